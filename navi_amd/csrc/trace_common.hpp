@@ -1,0 +1,74 @@
+// trace_common.hpp — device-side pieces shared by the tracer kernels.
+//
+// Semantics follow projects/torch-sdf/cpp_src/kernel.cu (paths relative to the
+// seismael/navi checkout); each helper cites the lines it restates. Every
+// floating-point operation is a single IEEE-754 binary32 operation: the library
+// is built with -ffp-contract=off and the one contraction the reference build
+// makes (p = o + t*d, kernel.cu:261-263) is written as an explicit fma.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace navi {
+
+constexpr float kOutsideDomain = 1000.0f;   // kernel.cuh:8
+constexpr float kDirEps = 1e-4f;            // kernel.cuh:9
+constexpr int kPrefixDepth = 4;             // kernel.cuh:11
+constexpr float kVoidAdvanceEps = 1e-5f;    // kernel.cu:9
+constexpr int kMaxDepth = 32;               // kernel.cu:136
+
+struct Box {
+    float x0, y0, z0, x1, y1, z1;
+};
+
+// kernel.cu:11-21 (inclusive)
+__device__ __forceinline__ bool in_box(float px, float py, float pz, const Box& b) {
+    return px >= b.x0 && px <= b.x1 && py >= b.y0 && py <= b.y1 && pz >= b.z0 && pz <= b.z1;
+}
+
+// kernel.cu:23-33 (strict)
+__device__ __forceinline__ bool in_box_strict(float px, float py, float pz, const Box& b) {
+    return px > b.x0 && px < b.x1 && py > b.y0 && py < b.y1 && pz > b.z0 && pz < b.z1;
+}
+
+// kernel.cu:43-47: binary16 -> binary32 (exact; v_cvt_f32_f16 keeps f16 denormals).
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits & 0xffffu)));
+}
+
+// kernel.cu:54-85
+__device__ __forceinline__ float exit_distance(float px, float py, float pz, float dx, float dy,
+                                               float dz, const Box& b) {
+    float t = kOutsideDomain;
+    if (dx > kDirEps) {
+        t = fminf(t, (b.x1 - px) / dx);
+    } else if (dx < -kDirEps) {
+        t = fminf(t, (b.x0 - px) / dx);
+    }
+    if (dy > kDirEps) {
+        t = fminf(t, (b.y1 - py) / dy);
+    } else if (dy < -kDirEps) {
+        t = fminf(t, (b.y0 - py) / dy);
+    }
+    if (dz > kDirEps) {
+        t = fminf(t, (b.z1 - pz) / dz);
+    } else if (dz < -kDirEps) {
+        t = fminf(t, (b.z0 - pz) / dz);
+    }
+    return fmaxf(t, kVoidAdvanceEps);
+}
+
+// kernel.cu:165-176: split `cur` at its midpoint toward p; returns the octant.
+__device__ __forceinline__ uint32_t descend_octant(float px, float py, float pz, Box& cur) {
+    const float mx = (cur.x0 + cur.x1) * 0.5f;
+    const float my = (cur.y0 + cur.y1) * 0.5f;
+    const float mz = (cur.z0 + cur.z1) * 0.5f;
+    uint32_t oct = 0;
+    if (px >= mx) { oct |= 1u; cur.x0 = mx; } else { cur.x1 = mx; }
+    if (py >= my) { oct |= 2u; cur.y0 = my; } else { cur.y1 = my; }
+    if (pz >= mz) { oct |= 4u; cur.z0 = mz; } else { cur.z1 = mz; }
+    return oct;
+}
+
+}  // namespace navi

@@ -1,0 +1,153 @@
+"""MI355X replacement of the native module ``torch_sdf_backend``.
+
+Mirrors the pybind11 surface of ``projects/torch-sdf/cpp_src/bindings.cpp:112-120``
+(same name, same 11 arguments, same ``skip_direction_validation`` default) and
+the argument contract of ``cast_rays_forward`` (``bindings.cpp:43-110``): the
+same checks in the same order with the same messages, raised as
+``RuntimeError`` (what a failed ``TORCH_CHECK`` becomes in Python). The launch
+goes through the C ABI ``navi_cast_rays`` (``include/navi_trace.h``) on
+PyTorch's *current* HIP stream — the reference launches on the legacy default
+stream (``kernel.cu:320``) although its trainer calls it under side streams.
+
+Additions, all keyword-only so the positional contract is unchanged:
+``hit_epsilon`` (the reference's compile-time ``kHitEpsilon``, ``kernel.cuh:7``)
+and ``out_steps`` (an int32 ``[B, R]`` tensor receiving per-ray step counts).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import numpy as np
+import torch
+
+from . import _native
+
+_DIRECTION_NORM_EPS = 1e-4  # kernel.cuh:9
+HIT_EPSILON = 0.01  # kernel.cuh:7
+
+__all__ = ["cast_rays", "HIT_EPSILON"]
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _f32(value) -> float:
+    # pybind11 converts to C++ float before any check (bindings.cpp:50,51,84).
+    with np.errstate(over="ignore"):
+        return float(np.float32(float(value)))
+
+
+def _validate_bounds(bbox_min, bbox_max) -> None:  # bindings.cpp:10-21
+    _check(len(bbox_min) == 3, "bbox_min must contain exactly 3 floats")
+    _check(len(bbox_max) == 3, "bbox_max must contain exactly 3 floats")
+    for idx in range(3):
+        lo = _f32(bbox_min[idx])
+        hi = _f32(bbox_max[idx])
+        _check(math.isfinite(lo), "bbox_min must contain only finite floats")
+        _check(math.isfinite(hi), "bbox_max must contain only finite floats")
+        _check(lo < hi, "bbox_min entries must be strictly less than bbox_max entries")
+
+
+def _validate_direction_norms(dirs: torch.Tensor) -> None:  # bindings.cpp:23-34
+    norms = torch.sqrt(torch.sum(dirs * dirs, -1))
+    _check(bool(torch.isfinite(norms).all().item()), "dirs must contain only finite direction vectors")
+    max_error = float(torch.abs(norms - 1.0).amax().item())
+    _check(
+        max_error <= _DIRECTION_NORM_EPS,
+        f"dirs must be normalized within tolerance {_DIRECTION_NORM_EPS:g}; max error was {max_error:g}",
+    )
+
+
+def validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics, max_steps,
+                         max_distance, bbox_min, bbox_max, resolution) -> None:
+    """The TORCH_CHECK block of ``cast_rays_forward`` (bindings.cpp:57-86)."""
+    _check(dag_tensor.is_cuda, "dag_tensor must be a CUDA tensor")
+    _check(origins.is_cuda, "origins must be a CUDA tensor")
+    _check(dirs.is_cuda, "dirs must be a CUDA tensor")
+    _check(out_distances.is_cuda, "out_distances must be a CUDA tensor")
+    _check(out_semantics.is_cuda, "out_semantics must be a CUDA tensor")
+
+    _check(origins.is_contiguous(), "origins must be contiguous")
+    _check(dirs.is_contiguous(), "dirs must be contiguous")
+    _check(out_distances.is_contiguous(), "out_distances must be contiguous")
+    _check(out_semantics.is_contiguous(), "out_semantics must be contiguous")
+    # The reference C++ layer does not check this one (its Python layer does,
+    # backend.py:64-65); the kernel reads the words as one flat array.
+    _check(dag_tensor.is_contiguous(), "dag_tensor must be contiguous")
+
+    _check(dag_tensor.dtype == torch.int64, "dag_tensor must be int64")
+    _check(origins.dtype == torch.float32, "origins must be float32")
+    _check(dirs.dtype == torch.float32, "dirs must be float32")
+    _check(out_distances.dtype == torch.float32, "out_distances must be float32")
+    _check(out_semantics.dtype == torch.int32, "out_semantics must be int32")
+
+    _check(origins.dim() == 3 and origins.size(2) == 3, "origins must be [Batch, Rays, 3]")
+    _check(dirs.dim() == 3 and dirs.size(2) == 3, "dirs must be [Batch, Rays, 3]")
+    _check(tuple(dirs.shape) == tuple(origins.shape), "dirs must match origins shape")
+    _check(out_distances.dim() == 2, "out_distances must be [Batch, Rays]")
+    _check(out_semantics.dim() == 2, "out_semantics must be [Batch, Rays]")
+    _check(
+        out_distances.size(0) == origins.size(0) and out_distances.size(1) == origins.size(1),
+        "out_distances must match the [Batch, Rays] shape of origins",
+    )
+    _check(
+        out_semantics.size(0) == origins.size(0) and out_semantics.size(1) == origins.size(1),
+        "out_semantics must match the [Batch, Rays] shape of origins",
+    )
+    _check(int(max_steps) > 0, "max_steps must be a positive integer")
+    _check(
+        math.isfinite(_f32(max_distance)) and _f32(max_distance) > 0.0,
+        "max_distance must be a finite positive float",
+    )
+    _check(int(resolution) > 0, "resolution must be a positive integer")
+    _validate_bounds(bbox_min, bbox_max)
+    # One device for every operand: the kernel dereferences all of them.
+    dev = dag_tensor.device
+    for name, t in (("origins", origins), ("dirs", dirs), ("out_distances", out_distances),
+                    ("out_semantics", out_semantics)):
+        _check(t.device == dev, f"{name} must be on the same device as dag_tensor ({dev})")
+
+
+def cast_rays(
+    dag_tensor: torch.Tensor,
+    origins: torch.Tensor,
+    dirs: torch.Tensor,
+    out_distances: torch.Tensor,
+    out_semantics: torch.Tensor,
+    max_steps: int,
+    max_distance: float,
+    bbox_min: list[float],
+    bbox_max: list[float],
+    resolution: int,
+    skip_direction_validation: bool = False,
+    *,
+    hit_epsilon: float = HIT_EPSILON,
+    out_steps: Any | None = None,
+) -> None:
+    """Batched bounded stackless sphere tracing (bindings.cpp:112-120 surface)."""
+    validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics, max_steps,
+                         max_distance, bbox_min, bbox_max, resolution)
+    if out_steps is not None:
+        _check(out_steps.is_cuda and out_steps.dtype == torch.int32 and out_steps.is_contiguous()
+               and tuple(out_steps.shape) == tuple(out_distances.shape)
+               and out_steps.device == dag_tensor.device,
+               "out_steps must be a contiguous int32 CUDA tensor shaped like out_distances")
+    if not skip_direction_validation:
+        _validate_direction_norms(dirs)
+
+    n_rays = int(origins.size(0)) * int(origins.size(1))
+    dev = dag_tensor.device
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        code = _native.lib().navi_cast_rays(
+            dag_tensor.data_ptr(), int(dag_tensor.numel()), origins.data_ptr(), dirs.data_ptr(),
+            out_distances.data_ptr(), out_semantics.data_ptr(), n_rays, int(max_steps),
+            float(max_distance), _native.float3(bbox_min), _native.float3(bbox_max),
+            int(resolution), float(hit_epsilon),
+            out_steps.data_ptr() if out_steps is not None else None, stream,
+        )
+    _native.check(code)
