@@ -1,0 +1,257 @@
+"""Throughput of the batched .gmdag sphere tracer on one MI355X.
+
+Workload (default): 16 seeded procedural scenes compiled at 1024^3 and all
+resident on the GPU (8 cluttered volumes, 8 room grids; seeds 100..115),
+1024 envs each assigned a scene id by seed, 256 x 48 rays per env
+(12,582,912 rays per step), max 256 steps, max distance 30 m, hit epsilon 0.01.
+A "step" is one trace of every ray of the batch, inputs already in HBM.
+
+Prints one JSON line: rays/s, the dominant kernel's roofline (algorithmic bytes
+per launch / HIP-event launch time vs the 8 TB/s HBM peak), the CPU oracle
+timed on a bounded sample on the host cores, and the parity of that sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+AZ, EL = 256, 48
+
+
+def _cache_dir() -> Path | None:
+    d = os.environ.get("NAVI_SCENE_CACHE", str(ROOT / ".scene_cache"))
+    if d in ("", "0", "off"):
+        return None
+    p = Path(d)
+    p.mkdir(parents=True, exist_ok=True)
+    return p
+
+
+def build_corpus(seeds, resolution, threads_total):
+    from navi_amd import scenes as S
+
+    cache = _cache_dir()
+    corpus = [S.corpus_scene(int(s), resolution) for s in seeds]
+    per = max(1, threads_total // 4)
+
+    def work(sc_seed):
+        sc, seed = sc_seed
+        path = cache / f"{sc.name}_{seed}_{resolution}.npy" if cache else None
+        if path is not None and path.exists():
+            sc.words = np.load(path)
+        else:
+            sc.compile(threads=per)
+            if path is not None:
+                np.save(path, sc.words)
+        return sc
+
+    with cf.ThreadPoolExecutor(max_workers=4) as ex:
+        corpus = list(ex.map(work, zip(corpus, seeds)))
+    return corpus
+
+
+def make_rays(corpus, n_envs, seed=4):
+    from navi_amd import scenes as S
+
+    rng = np.random.default_rng(seed)
+    env_scene = rng.integers(0, len(corpus), n_envs).astype(np.int32)
+    yaw = rng.uniform(0.0, 2.0 * math.pi, n_envs)
+    origins = np.empty((n_envs, 3), np.float32)
+    for s in range(len(corpus)):
+        idx = np.flatnonzero(env_scene == s)
+        if idx.size:
+            origins[idx] = corpus[s].free_origins(rng, idx.size)
+    local = S.canonical_directions(AZ, EL)
+    return env_scene, origins, yaw, local
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--envs", type=int, default=1024)
+    ap.add_argument("--resolution", type=int, default=1024)
+    ap.add_argument("--scenes", type=int, default=16)
+    ap.add_argument("--max-steps", type=int, default=256)
+    ap.add_argument("--max-distance", type=float, default=30.0)
+    ap.add_argument("--cpu-envs", type=int, default=256, help="envs in the CPU-baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-raw", action="store_true", help="skip timing the reference-layout kernel")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(rays shard by env with no exchange; see DESIGN.md)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import oracle
+    from navi_amd.multiscene import ResidentScenes
+
+    n_cpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    t0 = time.time()
+    seeds = list(range(100, 100 + args.scenes))
+    corpus = build_corpus(seeds, args.resolution, n_cpu)
+    t_compile = time.time() - t0
+    print(f"[bench] compiled {len(corpus)} scenes @{args.resolution}^3 in {t_compile:.1f}s, "
+          f"{sum(c.words.size for c in corpus) * 8 / 1e6:.1f} MB of words", file=sys.stderr, flush=True)
+
+    env_scene, origins_env, yaw, local = make_rays(corpus, args.envs)
+    from navi_amd import scenes as S
+
+    dirs = S.world_directions(local, yaw)
+    origins = np.ascontiguousarray(np.broadcast_to(origins_env[:, None, :], dirs.shape))
+
+    dev = torch.device("cuda:0")
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus], dev)
+    t_es = torch.from_numpy(env_scene).to(dev)
+    t_o = torch.from_numpy(origins).to(dev)
+    t_d = torch.from_numpy(dirs).to(dev)
+    E, R = dirs.shape[:2]
+    n_rays = E * R
+    out_d = torch.empty((E, R), device=dev)
+    out_s = torch.empty((E, R), device=dev, dtype=torch.int32)
+    out_n = torch.empty((E, R), device=dev, dtype=torch.int32)
+    out_w = torch.empty((E, R), device=dev, dtype=torch.int32)
+
+    def step(kernel="relaid"):
+        res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, kernel=kernel,
+                      elevation_bins=EL)
+
+    def timed(kernel, steps, warmup):
+        for _ in range(warmup):
+            step(kernel)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(steps):
+            step(kernel)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / steps
+
+    # untimed: counts of words the reference algorithm loads, and step counts
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_steps=out_n,
+                  out_words=out_w)
+    torch.cuda.synchronize()
+    total_words = int(out_w.to(torch.int64).sum().item())
+    mean_steps = float(out_n.float().mean().item())
+    hit_rate = float((out_s != 0).float().mean().item())
+
+    ms_raw = timed("raw", max(1, args.steps // 4), 1) if not args.no_raw else None
+    ms = timed("relaid", args.steps, args.warmup)
+    rays_per_s = n_rays / (ms / 1e3)
+
+    alg_bytes = n_rays * (24 + 8) + 8 * total_words
+    achieved_gbs = alg_bytes / (ms / 1e3) / 1e9
+
+    # CPU baseline + parity on a bounded sample: the first env of each scene
+    cpu = None
+    parity = None
+    if not args.no_cpu:
+        sample = []
+        for s in range(len(corpus)):
+            idx = np.flatnonzero(env_scene == s)
+            sample.extend(idx[: max(1, args.cpu_envs // len(corpus))].tolist())
+        sample = np.array(sorted(sample)[: max(args.cpu_envs, len(corpus))])
+        pool = np.concatenate([c.words for c in corpus])
+        base = np.cumsum([0] + [c.words.size for c in corpus[:-1]]).astype(np.uint64)
+        nw = np.array([c.words.size for c in corpus], np.uint64)
+        bounds = np.array([c.bbox_min_list + c.bbox_max for c in corpus], np.float32)
+        o_s, d_s, es_s = origins[sample], dirs[sample], env_scene[sample]
+        threads = n_cpu
+
+        def run_cpu():
+            return oracle.trace_multi(pool, base, nw, bounds, es_s, o_s, d_s, args.max_steps,
+                                      args.max_distance, threads=threads)
+
+        ref = run_cpu()  # warm-up
+        times = []
+        for _ in range(3):
+            t = time.perf_counter()
+            run_cpu()
+            times.append(time.perf_counter() - t)
+        t_cpu = float(np.median(times))
+        cpu = {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
+               "kind": "port",
+               "sample": f"{sample.size} envs x {R} rays = {sample.size * R} rays (the first "
+                         f"{max(1, args.cpu_envs // len(corpus))} envs of each of the {len(corpus)} "
+                         f"scenes), median of 3 timed runs after 1 warm-up"}
+        gd = out_d.cpu().numpy()[sample]
+        gs = out_s.cpu().numpy()[sample]
+        gn = out_n.cpu().numpy()[sample]
+        gw = out_w.cpu().numpy()[sample]
+        both_nan = np.isnan(gd) & np.isnan(ref["distance"])
+        dd = np.where(both_nan, 0.0, np.abs(gd.astype(np.float64) - ref["distance"]))
+        parity = {
+            "rays": int(gd.size),
+            "hit_mismatch": int(np.sum((gs != 0) != (ref["semantic"] != 0))),
+            "semantic_mismatch": int(np.sum(gs != ref["semantic"])),
+            "steps_mismatch": int(np.sum(gn != ref["steps"])),
+            "words_mismatch": int(np.sum(gw.astype(np.uint64) != ref["words"])),
+            "max_abs_dd": float(np.nanmax(dd)),
+            "bit_exact_distance": int(np.sum((gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both_nan)),
+        }
+
+    line = {
+        "metric": "rays/sec on 1 MI355X (256x48 rays/env)",
+        "value": round(rays_per_s, 1),
+        "unit": "rays/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded procedural scenes and poses)",
+        "config": {
+            "workload": f"{len(corpus)} resident scenes @{args.resolution}^3 (seeds {seeds[0]}..{seeds[-1]}), "
+                        f"{E} envs x {AZ}x{EL} rays, max {args.max_steps} steps, max {args.max_distance} m",
+            "envs": E, "rays_per_env": R, "rays_per_step": n_rays, "scenes": len(corpus),
+            "resolution": args.resolution, "max_steps": args.max_steps,
+            "max_distance": args.max_distance, "hit_epsilon": 0.01,
+            "entry_point": "navi_trace_relaid", "dag_bytes": res.pool_bytes,
+            "record_bytes": res.record_bytes,
+            "raw_layout_kernel_rays_per_s": None if ms_raw is None else round(n_rays / (ms_raw / 1e3), 1),
+            "mean_steps_per_ray": round(mean_steps, 3), "hit_rate": round(hit_rate, 4),
+            "dag_words_per_ray": round(total_words / n_rays, 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "trace_relaid_kernel",
+            "algorithmic_bytes_per_launch": alg_bytes,
+        },
+        "cpu_baseline": cpu,
+        "parity": parity,
+        "scene_compile_s": round(t_compile, 2),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

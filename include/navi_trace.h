@@ -39,6 +39,9 @@ extern "C" {
  *   n_rays       int64 (the reference narrows B*R to int, bindings.cpp:91);
  *   hit_epsilon  the reference's compile-time kHitEpsilon (pass 0.01f);
  *   out_steps    optional [n_rays] int32 march-loop iteration counts, or NULL;
+ *   out_words    optional [n_rays] uint32 counts of DAG words the reference
+ *                algorithm loads (load_dag_word calls, kernel.cu:137,198), or
+ *                NULL (a separate, slower kernel instance when non-NULL);
  *   stream       the caller's current stream (the reference launches on the
  *                legacy default stream, kernel.cu:320).
  * origins/dirs are [n_rays][3] float32, out_distances [n_rays] float32,
@@ -47,7 +50,73 @@ extern "C" {
 int navi_cast_rays(const uint64_t* dag, uint64_t n_words, const float* origins, const float* dirs,
                    float* out_distances, int32_t* out_semantics, int64_t n_rays, int32_t max_steps,
                    float max_distance, const float bbox_min[3], const float bbox_max[3],
-                   int32_t resolution, float hit_epsilon, int32_t* out_steps, void* stream);
+                   int32_t resolution, float hit_epsilon, int32_t* out_steps, uint32_t* out_words,
+                   void* stream);
+
+/* One resident scene of a multi-scene word pool (device memory, 40 bytes). */
+typedef struct navi_scene_desc {
+    uint64_t word_offset; /* first word of this scene's DAG in the pool */
+    uint64_t n_words;     /* its word count; child pointers are relative to word_offset */
+    float bbox_min[3];
+    float bbox_max[3];
+} navi_scene_desc;
+
+/*
+ * Trace n_envs * rays_per_env rays against several resident scenes in one
+ * launch: env e traces scenes[env_scene[e]]. The reference holds one DAG per
+ * call (projects/environment/src/navi_environment/backends/sdfdag_backend.py:
+ * 1897-1905) and its equivalent of this call is one cast_rays per scene over
+ * that scene's env subset (sdfdag_backend.py:1215-1217). `scenes` and
+ * `env_scene` are device arrays; an env whose scene id is out of range
+ * reports NaN / 0 / 0 steps. Outputs as in navi_cast_rays.
+ */
+int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, int32_t n_scenes,
+                         const int32_t* env_scene, int64_t n_envs, int64_t rays_per_env,
+                         const float* origins, const float* dirs, float* out_distances,
+                         int32_t* out_semantics, int32_t max_steps, float max_distance,
+                         float hit_epsilon, int32_t* out_steps, uint32_t* out_words, void* stream);
+
+/*
+ * Device layout (no reference counterpart; it replaces how the reference reads
+ * its words, kernel.cu:35-41,137-198). Converts a DAG in the reference word
+ * layout (host memory) into 32-byte records of eight u32 octant slots in
+ * breadth-first order: 0x7fffffff void, 0x7ffffffe out-of-range child, bit 31
+ * set = leaf inlined (bits 30..16 semantic, 15..0 fp16 distance), else a
+ * record index. With out_records NULL only counts; otherwise writes up to
+ * cap_records records. *root_slot is the root's slot value (0 = record 0, or
+ * an inlined leaf). n_levels_prefix (optional, 8 entries) receives the number
+ * of records at depth <= l. Returns NAVI_E_LAYOUT for DAGs with a reachable
+ * leaf semantic above 0x7fff (trace those with navi_cast_rays*).
+ */
+int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
+                  uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix);
+
+/* One resident scene in the device layout (device memory, 40 bytes). */
+typedef struct navi_relaid_scene {
+    uint64_t rec_offset;  /* first record of this scene in the record pool */
+    uint32_t n_records;
+    uint32_t root_slot;   /* from navi_relayout */
+    float bbox_min[3];
+    float bbox_max[3];
+} navi_relaid_scene;
+
+/*
+ * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
+ * traces scenes[env_scene ? env_scene[e] : 0]. Per-ray results are identical
+ * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
+ * (optional, a permutation of [0, n_envs)) is the order envs are swept in —
+ * pass envs sorted by scene id so resident scenes stream through the caches
+ * one at a time. elevation_bins > 0 (a multiple of 8 dividing rays_per_env / 8)
+ * declares the canonical az*El + el ray layout (projects/environment/src/
+ * navi_environment/backends/sdfdag_backend.py:205-221) so rays are traced in
+ * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
+ */
+int navi_trace_relaid(const uint32_t* records, const navi_relaid_scene* scenes, int32_t n_scenes,
+                      const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
+                      int64_t rays_per_env, int32_t elevation_bins, const float* origins,
+                      const float* dirs, float* out_distances, int32_t* out_semantics,
+                      int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
+                      void* stream);
 
 /* Message of the last failure on the calling thread ("" if none). The
  * reference surfaces failures as c10::Error via TORCH_CHECK (bindings.cpp:57-89). */

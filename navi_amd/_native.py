@@ -39,8 +39,50 @@ _lib.navi_version.argtypes = []
 _lib.navi_cast_rays.restype = ctypes.c_int
 _lib.navi_cast_rays.argtypes = [
     _vp, ctypes.c_uint64, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_float,
-    _f3, _f3, ctypes.c_int32, ctypes.c_float, _vp, _vp,
+    _f3, _f3, ctypes.c_int32, ctypes.c_float, _vp, _vp, _vp,
 ]
+_lib.navi_cast_rays_multi.restype = ctypes.c_int
+_lib.navi_cast_rays_multi.argtypes = [
+    _vp, _vp, ctypes.c_int32, _vp, ctypes.c_int64, ctypes.c_int64, _vp, _vp, _vp, _vp,
+    ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp, _vp,
+]
+
+_u64p = ctypes.POINTER(ctypes.c_uint64)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_lib.navi_relayout.restype = ctypes.c_int
+_lib.navi_relayout.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p, _u32p, _vp]
+_lib.navi_trace_relaid.restype = ctypes.c_int
+_lib.navi_trace_relaid.argtypes = [
+    _vp, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, _vp,
+    _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
+]
+
+# Layout of navi_relaid_scene (include/navi_trace.h), 40 bytes.
+RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot", "<u4"),
+                      ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,))]
+
+
+def relayout(words):
+    """Host conversion to the device record layout: returns
+    ``(records uint32 [n, 8], root_slot, levels_prefix[8])``; raises RuntimeError
+    (NAVI_E_LAYOUT) for DAGs the layout cannot hold."""
+    import numpy as np
+
+    w = np.ascontiguousarray(np.asarray(words).view(np.uint64).reshape(-1))
+    n = ctypes.c_uint64()
+    root = ctypes.c_uint32()
+    levels = np.zeros(8, np.uint64)
+    check(_lib.navi_relayout(w.ctypes.data, w.size, None, 0, ctypes.byref(n), ctypes.byref(root),
+                             levels.ctypes.data))
+    rec = np.zeros((max(1, n.value), 8), np.uint32)
+    check(_lib.navi_relayout(w.ctypes.data, w.size, rec.ctypes.data, n.value, ctypes.byref(n),
+                             ctypes.byref(root), levels.ctypes.data))
+    return rec[: n.value], int(root.value), levels
+
+
+# Layout of navi_scene_desc (include/navi_trace.h), 40 bytes.
+SCENE_DESC_DTYPE = [("word_offset", "<u8"), ("n_words", "<u8"), ("bbox_min", "<f4", (3,)),
+                    ("bbox_max", "<f4", (3,))]
 
 
 def lib() -> ctypes.CDLL:

@@ -39,15 +39,43 @@ __device__ __forceinline__ uint64_t load_word(const uint64_t* __restrict__ dag, 
     return dag[idx];
 }
 
+// Scene lookup for the raw-layout kernels: the single-scene entry point passes
+// one descriptor by value; the multi-scene one reads env_scene[ray / R].
+struct RawScene {
+    const uint64_t* words;
+    uint64_t n_words;
+    Box dom;
+    bool valid;
+};
+
 // One lane per ray; the loop body is kernel.cu:260-305 with query_dag_stackless
-// (kernel.cu:88-200) inlined.
+// (kernel.cu:88-200) inlined. kMulti: per-env scene table. kCount: also count
+// the DAG words the reference algorithm loads (kernel.cu:137,198) per ray.
+template <bool kMulti, bool kCount>
 __global__ __launch_bounds__(256) void trace_raw_kernel(
-    const uint64_t* __restrict__ dag, uint64_t n_words, const float* __restrict__ origins,
-    const float* __restrict__ dirs, float* __restrict__ out_d, int32_t* __restrict__ out_s,
-    int32_t* __restrict__ out_steps, int64_t n_rays, int32_t max_steps, float max_distance, Box dom,
+    const uint64_t* __restrict__ pool, uint64_t n_words, Box dom0,
+    const navi_scene_desc* __restrict__ scenes, int32_t n_scenes, const int32_t* __restrict__ env_scene,
+    int64_t rays_per_env, const float* __restrict__ origins, const float* __restrict__ dirs,
+    float* __restrict__ out_d, int32_t* __restrict__ out_s, int32_t* __restrict__ out_steps,
+    uint32_t* __restrict__ out_words, int64_t n_rays, int32_t max_steps, float max_distance,
     float hit_eps) {
     const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i >= n_rays) return;
+
+    RawScene sc{pool, n_words, dom0, true};
+    if constexpr (kMulti) {
+        const int32_t s = env_scene[i / rays_per_env];
+        if (s < 0 || s >= n_scenes) {
+            sc.valid = false;
+        } else {
+            const navi_scene_desc d = scenes[s];
+            sc.words = pool + d.word_offset;
+            sc.n_words = d.n_words;
+            sc.dom = Box{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2], d.bbox_max[0], d.bbox_max[1], d.bbox_max[2]};
+        }
+    }
+    const uint64_t* __restrict__ dag = sc.words;
+    const Box dom = sc.dom;
 
     const float ox = origins[3 * i + 0], oy = origins[3 * i + 1], oz = origins[3 * i + 2];
     const float dx = dirs[3 * i + 0], dy = dirs[3 * i + 1], dz = dirs[3 * i + 2];
@@ -60,11 +88,12 @@ __global__ __launch_bounds__(256) void trace_raw_kernel(
     bool pre_ok = false, vd_ok = false, lf_ok = false;
     float lf_dist = 0.0f;
     int32_t lf_sem = 0;
-    bool fault = false;
+    bool fault = !sc.valid;
     bool hit = false;
     int32_t steps = 0;
+    uint32_t words = 0;
 
-    for (int32_t step = 0; step < max_steps; ++step) {
+    for (int32_t step = 0; step < max_steps && !fault; ++step) {
         steps = step + 1;
         const float px = __builtin_fmaf(t, dx, ox);
         const float py = __builtin_fmaf(t, dy, oy);
@@ -83,7 +112,8 @@ __global__ __launch_bounds__(256) void trace_raw_kernel(
             uint32_t ptr = use_pre ? pre_ptr : 0u;
             Box cur = use_pre ? pre : dom;
             for (int depth = use_pre ? kPrefixDepth : 0; depth < kMaxDepth; ++depth) {
-                const uint64_t node = load_word(dag, n_words, ptr, fault);
+                if constexpr (kCount) ++words;
+                const uint64_t node = load_word(dag, sc.n_words, ptr, fault);
                 if (fault) break;
                 if (node >> 63) {  // leaf, kernel.cu:139-152
                     lf = cur;
@@ -110,7 +140,8 @@ __global__ __launch_bounds__(256) void trace_raw_kernel(
                 }
                 const uint32_t slot = static_cast<uint32_t>(node) +
                                       static_cast<uint32_t>(__builtin_popcount(mask & ((1u << oct) - 1u)));
-                ptr = static_cast<uint32_t>(load_word(dag, n_words, slot, fault));
+                if constexpr (kCount) ++words;
+                ptr = static_cast<uint32_t>(load_word(dag, sc.n_words, slot, fault));
                 if (fault) break;
             }
             if (fault) break;
@@ -125,6 +156,36 @@ __global__ __launch_bounds__(256) void trace_raw_kernel(
     out_d[i] = fault ? __builtin_nanf("") : t;
     out_s[i] = (hit && !fault) ? sem : 0;
     if (out_steps) out_steps[i] = steps;
+    if constexpr (kCount) out_words[i] = words;
+}
+
+}  // namespace navi
+
+namespace navi {
+
+int launch_raw(const uint64_t* pool, uint64_t n_words, Box dom, const navi_scene_desc* scenes,
+               int32_t n_scenes, const int32_t* env_scene, int64_t rays_per_env, const float* origins,
+               const float* dirs, float* out_d, int32_t* out_s, int32_t* out_steps, uint32_t* out_words,
+               int64_t n_rays, int32_t max_steps, float max_distance, float hit_eps, void* stream) {
+    const int threads = 256;
+    const int64_t blocks = (n_rays + threads - 1) / threads;
+    if (blocks > 0x7fffffff) return set_error(NAVI_E_ARG, "too many rays for one launch");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid(static_cast<unsigned>(blocks)), block(threads);
+    const bool multi = scenes != nullptr;
+    const bool count = out_words != nullptr;
+#define NAVI_LAUNCH_RAW(M, C)                                                                       \
+    hipLaunchKernelGGL((trace_raw_kernel<M, C>), grid, block, 0, s, pool, n_words, dom, scenes,     \
+                       n_scenes, env_scene, rays_per_env, origins, dirs, out_d, out_s, out_steps, \
+                       out_words, n_rays, max_steps, max_distance, hit_eps)
+    if (multi && count) NAVI_LAUNCH_RAW(true, true);
+    else if (multi) NAVI_LAUNCH_RAW(true, false);
+    else if (count) NAVI_LAUNCH_RAW(false, true);
+    else NAVI_LAUNCH_RAW(false, false);
+#undef NAVI_LAUNCH_RAW
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    return NAVI_OK;
 }
 
 }  // namespace navi
@@ -140,7 +201,8 @@ const char* navi_version(void) { return "0.1.0"; }
 int navi_cast_rays(const uint64_t* dag, uint64_t n_words, const float* origins, const float* dirs,
                    float* out_distances, int32_t* out_semantics, int64_t n_rays, int32_t max_steps,
                    float max_distance, const float bbox_min[3], const float bbox_max[3],
-                   int32_t resolution, float hit_epsilon, int32_t* out_steps, void* stream) {
+                   int32_t resolution, float hit_epsilon, int32_t* out_steps, uint32_t* out_words,
+                   void* stream) {
     g_last_error[0] = '\0';
     // Same contract as bindings.cpp:83-86 and :10-21.
     if (max_steps <= 0) return set_error(NAVI_E_ARG, "max_steps must be a positive integer");
@@ -162,16 +224,30 @@ int navi_cast_rays(const uint64_t* dag, uint64_t n_words, const float* origins, 
         return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
 
     const Box dom{bbox_min[0], bbox_min[1], bbox_min[2], bbox_max[0], bbox_max[1], bbox_max[2]};
-    const int threads = 256;
-    const int64_t blocks = (n_rays + threads - 1) / threads;
-    if (blocks > 0x7fffffff) return set_error(NAVI_E_ARG, "too many rays for one launch");
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    hipLaunchKernelGGL(trace_raw_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, s, dag,
-                       n_words, origins, dirs, out_distances, out_semantics,
-                       out_steps, n_rays, max_steps, max_distance, dom, hit_epsilon);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
-    return NAVI_OK;
+    return launch_raw(dag, n_words, dom, nullptr, 0, nullptr, 1, origins, dirs, out_distances,
+                      out_semantics, out_steps, out_words, n_rays, max_steps, max_distance, hit_epsilon,
+                      stream);
+}
+
+int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, int32_t n_scenes,
+                         const int32_t* env_scene, int64_t n_envs, int64_t rays_per_env,
+                         const float* origins, const float* dirs, float* out_distances,
+                         int32_t* out_semantics, int32_t max_steps, float max_distance,
+                         float hit_epsilon, int32_t* out_steps, uint32_t* out_words, void* stream) {
+    g_last_error[0] = '\0';
+    if (max_steps <= 0) return set_error(NAVI_E_ARG, "max_steps must be a positive integer");
+    if (!std::isfinite(max_distance) || !(max_distance > 0.0f))
+        return set_error(NAVI_E_ARG, "max_distance must be a finite positive float");
+    if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
+    if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
+    if (n_scenes <= 0 || !scenes || !pool || !env_scene) return set_error(NAVI_E_ARG, "scene table must be non-empty");
+    const int64_t n_rays = n_envs * rays_per_env;
+    if (n_rays == 0) return NAVI_OK;
+    if (!origins || !dirs || !out_distances || !out_semantics)
+        return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
+    return launch_raw(pool, 0, Box{}, scenes, n_scenes, env_scene, rays_per_env, origins, dirs,
+                      out_distances, out_semantics, out_steps, out_words, n_rays, max_steps,
+                      max_distance, hit_epsilon, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,129 @@
+// relayout.cpp — host-side conversion of the reference DAG word layout into the
+// tracer's device layout (part of libnavi_trace.so).
+//
+// Reference layout (docs/GMDAG.md:161-228, projects/torch-sdf/cpp_src/kernel.cu:
+// 137-198 of the seismael/navi checkout): u64 words; a leaf has bit 63 set, its
+// semantic in bits 31..16 and an fp16 distance in bits 15..0; an internal node
+// has a child mask in bits 62..55 and a child-table base in bits 31..0, the
+// table holding popcount(mask) words whose low 32 bits index the child.
+// Descending one level costs two dependent loads (node, then table slot).
+//
+// Device layout: one 32-byte record per reachable internal node, records in
+// breadth-first order from the root (so the top levels are a contiguous
+// prefix), each holding eight u32 slots indexed by octant:
+//   0x7fffffff             void octant (mask bit clear)
+//   0x7ffffffe             the reference would read past the array here
+//   bit 31 set             leaf inlined: bits 30..16 semantic, 15..0 fp16 distance
+//   otherwise              index of the child's record
+// Descending one level is one 4-byte load at record*8 + octant, and a leaf
+// costs no load of its own. Traversal semantics are unchanged: the tracer's
+// caches key on boxes, which depend only on the tree shape.
+//
+// Not representable (NAVI_E_LAYOUT; use the reference-layout kernel): a leaf
+// reachable from the root with semantic > 0x7fff, or more than 0x7ffffffd
+// internal nodes.
+#include <stdint.h>
+
+#include <cstring>
+#include <vector>
+
+#include "navi_trace.h"
+
+namespace navi {
+int set_error(int code, const char* fmt, ...);
+}
+
+namespace {
+
+constexpr uint32_t kSlotVoid = 0x7fffffffu;
+constexpr uint32_t kSlotFault = 0x7ffffffeu;
+constexpr uint32_t kUnassigned = 0xffffffffu;
+
+// Slot value for a child word index, assigning record ids on first sight.
+inline bool child_slot(const uint64_t* w, uint64_t n, uint32_t idx, std::vector<uint32_t>& rec_of,
+                       std::vector<uint32_t>& queue, uint32_t& out) {
+    if (static_cast<uint64_t>(idx) >= n) {
+        out = kSlotFault;
+        return true;
+    }
+    const uint64_t node = w[idx];
+    if (node >> 63) {
+        const uint32_t sem = static_cast<uint32_t>(node >> 16) & 0xffffu;
+        if (sem > 0x7fffu) return false;
+        out = 0x80000000u | (sem << 16) | static_cast<uint32_t>(node & 0xffffu);
+        return true;
+    }
+    if (rec_of[idx] == kUnassigned) {
+        if (queue.size() >= kSlotFault) return false;
+        rec_of[idx] = static_cast<uint32_t>(queue.size());
+        queue.push_back(idx);
+    }
+    out = rec_of[idx];
+    return true;
+}
+
+}  // namespace
+
+extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records,
+                             uint64_t cap_records, uint64_t* n_records, uint32_t* root_slot,
+                             uint64_t* n_levels_prefix) {
+    using navi::set_error;
+    if (!words || n_words == 0) return set_error(NAVI_E_ARG, "dag must hold at least one word");
+    if (!n_records || !root_slot) return set_error(NAVI_E_ARG, "n_records and root_slot are required");
+    const uint64_t root = words[0];
+    if (root >> 63) {  // a one-leaf DAG: no records
+        const uint32_t sem = static_cast<uint32_t>(root >> 16) & 0xffffu;
+        if (sem > 0x7fffu) return set_error(NAVI_E_LAYOUT, "leaf semantic %u exceeds 15 bits", sem);
+        *root_slot = 0x80000000u | (sem << 16) | static_cast<uint32_t>(root & 0xffffu);
+        *n_records = 0;
+        if (n_levels_prefix) std::memset(n_levels_prefix, 0, 8 * sizeof(uint64_t));
+        return NAVI_OK;
+    }
+    std::vector<uint32_t> rec_of(n_words, kUnassigned);
+    std::vector<uint32_t> queue;
+    queue.reserve(1024);
+    rec_of[0] = 0;
+    queue.push_back(0);
+    *root_slot = 0;
+    // breadth-first: record r's children are assigned ids in octant order
+    size_t level_end = 1;
+    int level = 0;
+    if (n_levels_prefix) std::memset(n_levels_prefix, 0, 8 * sizeof(uint64_t));
+    for (size_t r = 0; r < queue.size(); ++r) {
+        if (r == level_end) {
+            if (n_levels_prefix && level < 8) n_levels_prefix[level] = level_end;
+            ++level;
+            level_end = queue.size();
+        }
+        const uint64_t node = words[queue[r]];
+        const uint32_t mask = static_cast<uint32_t>(node >> 55) & 0xffu;
+        const uint32_t base = static_cast<uint32_t>(node);
+        uint32_t slots[8];
+        uint32_t k = 0;
+        for (uint32_t oct = 0; oct < 8; ++oct) {
+            if (!(mask & (1u << oct))) {
+                slots[oct] = kSlotVoid;
+                continue;
+            }
+            const uint32_t tab = base + k;  // uint32 arithmetic, as kernel.cu:197
+            ++k;
+            if (static_cast<uint64_t>(tab) >= n_words) {
+                slots[oct] = kSlotFault;
+                continue;
+            }
+            const uint32_t child = static_cast<uint32_t>(words[tab]);
+            if (!child_slot(words, n_words, child, rec_of, queue, slots[oct]))
+                return set_error(NAVI_E_LAYOUT, "DAG not representable in the device layout "
+                                                "(leaf semantic above 0x7fff or too many nodes)");
+        }
+        if (out_records) {
+            if (r >= cap_records) return set_error(NAVI_E_ARG, "record buffer too small");
+            std::memcpy(out_records + 8 * r, slots, sizeof slots);
+        }
+    }
+    if (n_levels_prefix) {
+        for (int l = level; l < 8; ++l) n_levels_prefix[l] = queue.size();
+    }
+    *n_records = queue.size();
+    return NAVI_OK;
+}

@@ -1,0 +1,152 @@
+"""Several ``.gmdag`` scenes resident on one GPU, traced in one launch.
+
+The reference keeps one DAG tensor per backend and swaps it on scene rotation
+(``projects/environment/src/navi_environment/backends/sdfdag_backend.py:864-886,
+1897-1905``); a batch over envs in different scenes costs one ``cast_rays`` per
+scene. Here all scenes live in one device word pool with a 40-byte descriptor
+each (``navi_scene_desc`` in ``include/navi_trace.h``) and an int32 scene id
+per env selects the DAG inside the kernel.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Sequence
+
+import numpy as np
+import torch
+
+from . import _native
+
+
+class ResidentScenes:
+    """Concatenated word pool + scene table on one device.
+
+    ``scenes`` is a sequence of ``(words, bbox_min, bbox_max)`` with ``words`` a
+    uint64 (or int64-viewed) array in the reference word layout; child pointers
+    stay relative to each scene's first word.
+    """
+
+    def __init__(self, scenes: Sequence[tuple[np.ndarray, Sequence[float], Sequence[float]]],
+                 device: str | torch.device = "cuda") -> None:
+        if not scenes:
+            raise ValueError("at least one scene is required")
+        self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        table = np.zeros(len(scenes), dtype=_native.SCENE_DESC_DTYPE)
+        offset = 0
+        chunks = []
+        for i, (words, lo, hi) in enumerate(scenes):
+            w = np.ascontiguousarray(np.asarray(words).view(np.uint64).reshape(-1))
+            if w.size == 0:
+                raise ValueError(f"scene {i} has no words")
+            for k in range(3):
+                if not (math.isfinite(float(lo[k])) and math.isfinite(float(hi[k])) and float(lo[k]) < float(hi[k])):
+                    raise ValueError(f"scene {i}: bbox_min must be finite and strictly below bbox_max")
+            table[i]["word_offset"] = offset
+            table[i]["n_words"] = w.size
+            table[i]["bbox_min"] = np.asarray(lo, np.float32)
+            table[i]["bbox_max"] = np.asarray(hi, np.float32)
+            chunks.append(w)
+            offset += w.size
+        self.n_scenes = len(scenes)
+        self.word_counts = [int(c.size) for c in chunks]
+        self.host_table = table
+        self.pool = torch.from_numpy(np.concatenate(chunks).view(np.int64)).to(self.device)
+        self.table = torch.from_numpy(table.view(np.uint8).copy()).to(self.device)
+
+        # device record layout (one 32-byte record per internal node)
+        rtable = np.zeros(len(scenes), dtype=_native.RELAID_SCENE_DTYPE)
+        recs = []
+        roff = 0
+        self.relaid_ok = True
+        for i, w in enumerate(chunks):
+            try:
+                rec, root, _levels = _native.relayout(w)
+            except RuntimeError:
+                self.relaid_ok = False
+                break
+            rtable[i]["rec_offset"] = roff
+            rtable[i]["n_records"] = rec.shape[0]
+            rtable[i]["root_slot"] = root
+            rtable[i]["bbox_min"] = table[i]["bbox_min"]
+            rtable[i]["bbox_max"] = table[i]["bbox_max"]
+            recs.append(rec)
+            roff += rec.shape[0]
+        if self.relaid_ok:
+            allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
+            self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)
+            self.relaid_table = torch.from_numpy(rtable.view(np.uint8).copy()).to(self.device)
+            self.record_counts = [int(r.shape[0]) for r in recs]
+        self._order_key = None
+        self._order = None
+
+    @property
+    def pool_bytes(self) -> int:
+        return int(self.pool.numel()) * 8
+
+    @property
+    def record_bytes(self) -> int:
+        return int(self.records.numel()) * 4 if self.relaid_ok else 0
+
+    def env_order(self, env_scene: torch.Tensor) -> torch.Tensor:
+        """Envs sorted (stably) by scene id, cached per env_scene contents/version."""
+        key = (env_scene.data_ptr(), env_scene._version, tuple(env_scene.shape))
+        if self._order_key != key:
+            self._order = torch.sort(env_scene.to(torch.int64), stable=True).indices.to(torch.int32)
+            self._order_key = key
+        return self._order
+
+    def cast_rays(self, env_scene: torch.Tensor, origins: torch.Tensor, dirs: torch.Tensor,
+                  out_distances: torch.Tensor, out_semantics: torch.Tensor, max_steps: int,
+                  max_distance: float, *, hit_epsilon: float = 0.01, out_steps: Any | None = None,
+                  out_words: Any | None = None, kernel: str = "relaid",
+                  elevation_bins: int | None = None, sort_by_scene: bool = True) -> None:
+        """Trace ``origins``/``dirs`` ``[E, R, 3]``; env ``e`` uses scene ``env_scene[e]``.
+        Outputs ``[E, R]`` are written in place on the current stream.
+
+        ``kernel="relaid"`` (default) runs the device-layout tracer; ``"raw"`` walks the
+        reference word layout (and is the one that can fill ``out_words``). Both give
+        identical per-ray results. ``elevation_bins`` declares the canonical
+        ``az * El + el`` ray layout for angular tiling."""
+        e, r = int(origins.shape[0]), int(origins.shape[1])
+        for name, t, dt, shape in (("origins", origins, torch.float32, (e, r, 3)),
+                                   ("dirs", dirs, torch.float32, (e, r, 3)),
+                                   ("out_distances", out_distances, torch.float32, (e, r)),
+                                   ("out_semantics", out_semantics, torch.int32, (e, r)),
+                                   ("env_scene", env_scene, torch.int32, (e,))):
+            if t.device != self.device or t.dtype != dt or not t.is_contiguous() or tuple(t.shape) != shape:
+                raise RuntimeError(f"{name} must be a contiguous {dt} tensor of shape {shape} on {self.device}")
+        for name, t, dt in (("out_steps", out_steps, torch.int32), ("out_words", out_words, torch.int32)):
+            if t is not None and (t.device != self.device or t.dtype != dt or not t.is_contiguous()
+                                  or tuple(t.shape) != (e, r)):
+                raise RuntimeError(f"{name} must be a contiguous {dt} tensor of shape {(e, r)}")
+        if int(max_steps) <= 0:
+            raise RuntimeError("max_steps must be a positive integer")
+        if not (math.isfinite(float(max_distance)) and float(max_distance) > 0.0):
+            raise RuntimeError("max_distance must be a finite positive float")
+        if kernel == "relaid" and out_words is None and self.relaid_ok:
+            order = self.env_order(env_scene) if sort_by_scene else None
+            with torch.cuda.device(self.device):
+                stream = torch.cuda.current_stream(self.device).cuda_stream
+                code = _native.lib().navi_trace_relaid(
+                    self.records.data_ptr(), self.relaid_table.data_ptr(), self.n_scenes,
+                    env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
+                    int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
+                    out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),
+                    float(max_distance), float(hit_epsilon),
+                    out_steps.data_ptr() if out_steps is not None else None, stream)
+            _native.check(code)
+            return
+        if kernel not in ("relaid", "raw"):
+            raise ValueError(f"unknown kernel {kernel!r}")
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            code = _native.lib().navi_cast_rays_multi(
+                self.pool.data_ptr(), self.table.data_ptr(), self.n_scenes, env_scene.data_ptr(), e, r,
+                origins.data_ptr(), dirs.data_ptr(), out_distances.data_ptr(), out_semantics.data_ptr(),
+                int(max_steps), float(max_distance), float(hit_epsilon),
+                out_steps.data_ptr() if out_steps is not None else None,
+                out_words.data_ptr() if out_words is not None else None, stream)
+        _native.check(code)

@@ -148,6 +148,6 @@ def cast_rays(
             out_distances.data_ptr(), out_semantics.data_ptr(), n_rays, int(max_steps),
             float(max_distance), _native.float3(bbox_min), _native.float3(bbox_max),
             int(resolution), float(hit_epsilon),
-            out_steps.data_ptr() if out_steps is not None else None, stream,
+            out_steps.data_ptr() if out_steps is not None else None, None, stream,
         )
     _native.check(code)

@@ -1,0 +1,212 @@
+"""GPU parity of the multi-scene entry points (reference-layout kernel and the
+device-layout throughput kernel) against the CPU oracle.
+
+Bar: hit/miss, semantic and step counts bit-exact, distance within
+1e-4 * max_distance (distances are expected bit-exact and counted), and the
+per-ray count of DAG words the reference algorithm loads bit-exact.
+"""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_gpu_trace import _full_octree_words
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).with_name("golden") / "known_answers.json"
+
+
+def _corpus():
+    from navi_amd import scenes as S
+
+    corpus = [S.box_room(seed=1, resolution=64), S.cluttered(seed=2, resolution=128),
+              S.rooms(seed=3, resolution=128), S.cluttered(seed=5, resolution=64)]
+    for c in corpus:
+        c.compile()
+    return corpus
+
+
+@pytest.fixture(scope="module")
+def corpus():
+    return _corpus()
+
+
+def _rays(corpus, n_envs, az, el, seed):
+    from navi_amd import scenes as S
+
+    rng = np.random.default_rng(seed)
+    env_scene = rng.integers(0, len(corpus), n_envs).astype(np.int32)
+    origins = np.empty((n_envs, 3), np.float32)
+    for s in range(len(corpus)):
+        idx = np.flatnonzero(env_scene == s)
+        if idx.size:
+            origins[idx] = corpus[s].free_origins(rng, idx.size)
+    dirs = S.world_directions(S.canonical_directions(az, el), rng.uniform(0, 2 * math.pi, n_envs))
+    o = np.ascontiguousarray(np.broadcast_to(origins[:, None, :], dirs.shape))
+    return env_scene, o, dirs
+
+
+def _oracle_multi(corpus_words, bounds, env_scene, o, d, max_steps, max_distance, hit_epsilon=0.01):
+    base = np.cumsum([0] + [w.size for w in corpus_words[:-1]]).astype(np.uint64)
+    nw = np.array([w.size for w in corpus_words], np.uint64)
+    return oracle.trace_multi(np.concatenate(corpus_words), base, nw, np.asarray(bounds, np.float32),
+                              env_scene, o, d, max_steps, max_distance, hit_epsilon, threads=8)
+
+
+def _run(res, env_scene, o, d, max_steps, max_distance, **kw):
+    import torch
+
+    dev = res.device
+    t_es = torch.from_numpy(np.ascontiguousarray(env_scene, np.int32)).to(dev)
+    t_o = torch.from_numpy(np.ascontiguousarray(o)).to(dev)
+    t_d = torch.from_numpy(np.ascontiguousarray(d)).to(dev)
+    shape = o.shape[:2]
+    out_d = torch.full(shape, -7.0, device=dev)
+    out_s = torch.full(shape, -7, device=dev, dtype=torch.int32)
+    out_n = torch.full(shape, -7, device=dev, dtype=torch.int32)
+    out_w = torch.full(shape, -7, device=dev, dtype=torch.int32) if kw.pop("count", False) else None
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, max_steps, max_distance, out_steps=out_n,
+                  out_words=out_w, **kw)
+    torch.cuda.synchronize()
+    return (out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(),
+            None if out_w is None else out_w.cpu().numpy())
+
+
+def _compare(got, ref, max_distance, label):
+    gd, gs, gn, gw = got
+    assert np.array_equal(gs != 0, ref["semantic"] != 0), f"{label}: hit mask"
+    assert np.array_equal(gs, ref["semantic"]), f"{label}: semantics"
+    assert np.array_equal(gn, ref["steps"]), f"{label}: steps differ on {np.sum(gn != ref['steps'])}"
+    assert np.array_equal(np.isnan(gd), np.isnan(ref["distance"])), f"{label}: NaN pattern"
+    both = np.isnan(gd) & np.isnan(ref["distance"])
+    dd = np.where(both, 0.0, np.abs(gd.astype(np.float64) - ref["distance"]))
+    assert float(dd.max(initial=0.0)) <= 1e-4 * max_distance, f"{label}: max |dd| {dd.max()}"
+    exact = (gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both
+    assert exact.all(), f"{label}: {np.sum(~exact)} distances not bit-exact"
+    if gw is not None:
+        assert np.array_equal(gw.astype(np.uint64), ref["words"]), f"{label}: word counts"
+
+
+@pytest.mark.parametrize("kernel,el_bins,sort", [("raw", None, False), ("relaid", None, False),
+                                                 ("relaid", 16, True), ("relaid", 16, False)])
+def test_multiscene_parity(gpu, corpus, kernel, el_bins, sort):
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    assert res.relaid_ok
+    env_scene, o, d = _rays(corpus, 40, 32, 16, seed=9)
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, o, d, 192, 30.0)
+    got = _run(res, env_scene, o, d, 192, 30.0, kernel=kernel, elevation_bins=el_bins,
+               sort_by_scene=sort, count=(kernel == "raw"))
+    _compare(got, ref, 30.0, f"{kernel}/{el_bins}/{sort}")
+
+
+def test_relaid_random_rays_and_short_budgets(gpu, corpus):
+    """Random origins (inside and outside the cubes) and directions, several max_steps."""
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    rng = np.random.default_rng(21)
+    n_env, rays = 12, 1000
+    env_scene = rng.integers(0, len(corpus), n_env).astype(np.int32)
+    lo = np.array([corpus[s].bbox_min_list for s in env_scene]) - 3.0
+    hi = np.array([corpus[s].bbox_max for s in env_scene]) + 3.0
+    o = rng.uniform(lo[:, None, :], hi[:, None, :], (n_env, rays, 3)).astype(np.float32)
+    d = rng.normal(size=(n_env, rays, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    for max_steps in (1, 7, 300):
+        ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                            env_scene, o, d, max_steps, 45.0)
+        _compare(_run(res, env_scene, o, d, max_steps, 45.0), ref, 45.0, f"random/{max_steps}")
+
+
+def test_unknown_scene_id_reports_nan(gpu, corpus):
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus[:2]])
+    env_scene, o, d = _rays(corpus[:2], 3, 8, 8, seed=2)
+    env_scene = np.array([0, 7, -1], np.int32)
+    for kernel in ("raw", "relaid"):
+        gd, gs, gn, _ = _run(res, env_scene, o, d, 64, 30.0, kernel=kernel)
+        assert np.isnan(gd[1:]).all() and (gs[1:] == 0).all() and (gn[1:] == 0).all(), kernel
+        assert not np.isnan(gd[0]).any(), kernel
+
+
+@pytest.mark.parametrize("case", json.loads(GOLDEN.read_text())["cases"], ids=lambda c: c["name"])
+def test_known_answers_both_kernels(gpu, case):
+    from navi_amd.multiscene import ResidentScenes
+
+    words = np.array([int(w, 16) for w in case["words"]], dtype=np.uint64)
+    res = ResidentScenes([(words, case["bbox_min"], case["bbox_max"])])
+    o = np.array(case["origins"], np.float32)[None]
+    d = np.array(case["dirs"], np.float32)[None]
+    ref = oracle.trace(words, o, d, case["max_steps"], case["max_distance"], case["bbox_min"],
+                       case["bbox_max"])
+    for kernel in ("raw", "relaid"):
+        got = _run(res, np.zeros(1, np.int32), o, d, case["max_steps"], case["max_distance"],
+                   kernel=kernel, count=(kernel == "raw"))
+        _compare(got, ref, case["max_distance"], f"{case['name']}/{kernel}")
+        for i, e in enumerate(case["expect"]):
+            assert int(got[1][0, i]) == e["semantic"]
+            if "atol" in e:
+                assert abs(float(got[0][0, i]) - e["distance"]) <= e["atol"]
+            else:
+                assert float(got[0][0, i]) > e["distance_gt"]
+
+
+def test_relaid_malformed_dags(gpu):
+    """Out-of-range child table and a self-cycle: the device layout keeps the
+    reference-layout kernel's fault (NaN) and depth-exhaustion (stale) results."""
+    from navi_amd.multiscene import ResidentScenes
+
+    oob = np.array([(0xFF << 55) | 1] + [50] * 8, dtype=np.uint64)
+    cyc = np.array([(0xFF << 55) | 1] + [0] * 8, dtype=np.uint64)
+    table_past_end = np.array([(0xFF << 55) | 5, 1, 2], dtype=np.uint64)
+    scenes = [(w, [0, 0, 0], [1, 1, 1]) for w in (oob, cyc, table_past_end)]
+    res = ResidentScenes(scenes)
+    rng = np.random.default_rng(4)
+    o = rng.uniform(-0.2, 1.2, (3, 64, 3)).astype(np.float32)
+    d = rng.normal(size=(3, 64, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    env_scene = np.arange(3, dtype=np.int32)
+    ref = _oracle_multi([s[0] for s in scenes], [[0, 0, 0, 1, 1, 1]] * 3, env_scene, o, d, 9, 10.0)
+    for kernel in ("raw", "relaid"):
+        _compare(_run(res, env_scene, o, d, 9, 10.0, kernel=kernel, count=(kernel == "raw")), ref, 10.0,
+                 f"malformed/{kernel}")
+
+
+def test_relaid_exhaustive_fp16_inline_leaves(gpu):
+    from navi_amd.multiscene import ResidentScenes
+
+    bits = np.arange(65536, dtype=np.uint32)
+    words, _ = _full_octree_words(6, bits)
+    res = ResidentScenes([(words, [0, 0, 0], [1, 1, 1])])
+    cells = np.arange(65536)
+    ix = np.zeros(65536, np.int64)
+    iy = np.zeros(65536, np.int64)
+    iz = np.zeros(65536, np.int64)
+    for lvl in range(6):
+        digit = (cells // (8 ** (5 - lvl))) % 8
+        ix, iy, iz = ix * 2 + (digit & 1), iy * 2 + ((digit >> 1) & 1), iz * 2 + ((digit >> 2) & 1)
+    o = ((np.stack([ix, iy, iz], -1) + 0.5) / 64).astype(np.float32)[None]
+    d = np.tile(np.array([1.0, 0.0, 0.0], np.float32), (1, 65536, 1))
+    gd, gs, gn, _ = _run(res, np.zeros(1, np.int32), o, d, 1, 3e38, kernel="relaid")
+    want = oracle.half_to_float(bits.astype(np.uint16)) + np.float32(0.0)
+    same = (gd[0].view(np.uint32) == want.view(np.uint32)) | (np.isnan(gd[0]) & np.isnan(want))
+    assert same.all()
+
+
+def test_relayout_rejects_wide_semantics(gpu):
+    from navi_amd import _native
+
+    words = np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], dtype=np.uint64)
+    with pytest.raises(RuntimeError, match="15 bits"):
+        _native.relayout(words)
