@@ -1,23 +1,30 @@
 // trace_relaid.hip — the throughput tracer over the device record layout
-// (relayout.cpp). Same per-ray results as the reference-layout kernel, which
-// restates projects/torch-sdf/cpp_src/kernel.cu:88-309 (seismael/navi checkout).
+// (relayout.cpp). Per-ray results are identical to the reference-layout kernel,
+// which restates projects/torch-sdf/cpp_src/kernel.cu:88-309 (seismael/navi
+// checkout); tests compare both against the CPU oracle bit for bit.
 //
 // Execution model (CDNA4, wave64):
 //   * persistent waves: the grid holds about as many waves as the chip keeps
 //     resident; wave w walks 64-ray chunks w, w + W, w + 2W, ... of the work
 //     order, so all waves sweep the batch front to back together;
-//   * lane refill: a lane whose ray finished takes the next ray of its wave's
-//     chunk sequence at once (ballot + prefix popcount), so a wave never idles
-//     on a few long rays;
-//   * if-if state machine: every loop iteration a lane either starts a march
-//     step (caches answer most of them without memory traffic) or descends one
-//     DAG level with a single 4-byte gather; lanes that finish a level or a
-//     cached step in the same iteration are not held back by deeper ones;
+//   * lane refill: at the top of every march step, lanes whose ray finished
+//     take the next rays of the wave's chunk sequence (ballot + prefix
+//     popcount), so a wave never idles on a few long rays;
+//   * one march step per outer iteration for every lane; the caches answer
+//     ~40% of steps with no memory traffic; the rest run a tight inner loop of
+//     one 4-byte gather per DAG level until every lane of the wave has found
+//     its leaf / void cell, then all lanes finish the step together;
 //   * work order: envs in the order given (callers sort them by scene so the
 //     resident scenes stream through L2 / MALL one or two at a time) and, when
 //     the elevation count is a multiple of 8, 8 x 8 (az x el) tiles of the
 //     canonical az*El + el ray layout, so a chunk's rays are angular
 //     neighbours that share DAG nodes.
+// Arithmetic: the void-cell exit divides (kernel.cu:54-85) use a per-ray
+// correctly rounded reciprocal and one Markstein correction,
+// q = fma(fma(-a*r, b, a), r, a*r), which equals the IEEE quotient a/b when
+// r = RN(1/b) and nothing over/underflows (|a| in [2^-60, 2^60], |b| in
+// [1e-4, 2^20]); other operands take the IEEE division. 32-bit work indexing with
+// multiply-high division by the (uniform) rays-per-env and tile counts.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -32,15 +39,39 @@ int set_error(int code, const char* fmt, ...);
 constexpr uint32_t kSlotVoid = 0x7fffffffu;
 constexpr uint32_t kSlotFault = 0x7ffffffeu;
 
+// Division by a runtime-invariant divisor d >= 1 (Granlund-Montgomery):
+// n / d = (t + ((n - t) >> 1)) >> (l - 1), t = mulhi(n, m), for all 32-bit n.
+struct FastDiv {
+    uint32_t d, m, l;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f{d, 0u, 0u};
+    if (d <= 1) return f;
+    uint32_t l = 0;
+    while ((1ull << l) < d) ++l;
+    f.l = l;
+    f.m = static_cast<uint32_t>(((1ull << 32) * ((1ull << l) - d)) / d + 1);
+    return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    if (f.d <= 1) return n;
+    const uint32_t t = __umulhi(n, f.m);
+    return (t + ((n - t) >> 1)) >> (f.l - 1);
+}
+
 struct RelaidParams {
     const uint32_t* __restrict__ records;
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
     const int32_t* __restrict__ env_order;  // null: identity
-    int64_t n_envs;
-    int64_t rays_per_env;
-    int32_t tile_el;  // elevation bins when 8x8 tiling applies, else 0
+    uint32_t n_rays;
+    uint32_t rays_per_env;
+    FastDiv div_rays;      // by rays_per_env
+    uint32_t tile_el;      // elevation bins when 8x8 tiling applies, else 0
+    FastDiv div_tiles_el;  // by tile_el / 8
     const float* __restrict__ origins;
     const float* __restrict__ dirs;
     float* __restrict__ out_d;
@@ -49,63 +80,69 @@ struct RelaidParams {
     int32_t max_steps;
     float max_distance;
     float hit_eps;
-    int64_t n_chunks;
+    uint32_t n_chunks;
 };
 
 // Work index q -> ray id (env * R + r).
-__device__ __forceinline__ int64_t ray_of(const RelaidParams& P, int64_t q, int32_t& env_out) {
-    const int64_t env_pos = q / P.rays_per_env;
-    const int64_t qi = q - env_pos * P.rays_per_env;
-    int64_t r = qi;
-    if (P.tile_el > 0) {
-        const int64_t tiles_el = P.tile_el >> 3;
-        const int64_t tile = qi >> 6;
-        const int64_t l = qi & 63;
-        const int64_t ta = tile / tiles_el;
-        const int64_t te = tile - ta * tiles_el;
-        r = (ta * 8 + (l & 7)) * P.tile_el + te * 8 + (l >> 3);
+__device__ __forceinline__ uint32_t ray_of(const RelaidParams& P, uint32_t q, int32_t& env_out) {
+    const uint32_t env_pos = fdiv(q, P.div_rays);
+    const uint32_t qi = q - env_pos * P.rays_per_env;
+    uint32_t r = qi;
+    if (P.tile_el) {
+        const uint32_t tile = qi >> 6;
+        const uint32_t l = qi & 63u;
+        const uint32_t ta = fdiv(tile, P.div_tiles_el);
+        const uint32_t te = tile - ta * (P.tile_el >> 3);
+        r = (ta * 8u + (l & 7u)) * P.tile_el + te * 8u + (l >> 3);
     }
     const int32_t env = P.env_order ? P.env_order[env_pos] : static_cast<int32_t>(env_pos);
     env_out = env;
-    return static_cast<int64_t>(env) * P.rays_per_env + r;
+    return static_cast<uint32_t>(env) * P.rays_per_env + r;
 }
 
-__device__ __forceinline__ float slot_dist(uint32_t s) { return half_to_float(s & 0xffffu); }
-__device__ __forceinline__ int32_t slot_sem(uint32_t s) { return static_cast<int32_t>((s >> 16) & 0x7fffu); }
+// a / b for the exit distance: Markstein-corrected product with r = RN(1/b).
+__device__ __forceinline__ float div_exact(float a, float b, float r) {
+    const float aa = fabsf(a);
+    if (__builtin_expect(aa >= 0x1p-60f && aa <= 0x1p60f && fabsf(b) <= 0x1p20f, 1)) {
+        const float q0 = a * r;
+        const float e = __builtin_fmaf(-q0, b, a);
+        return __builtin_fmaf(e, r, q0);
+    }
+    return a / b;
+}
+
+enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
 
 __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
     const uint32_t lane = threadIdx.x & 63u;
-    const int64_t wave = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
-    const int64_t n_waves = (static_cast<int64_t>(gridDim.x) * blockDim.x) >> 6;
-    const int64_t n_rays = P.n_envs * P.rays_per_env;
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
     // this wave's chunks: wave, wave + n_waves, ...
-    const int64_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0;
-    const int64_t seq_end = my_chunks * 64;
-    int64_t seq_next = 0;  // wave-uniform
+    const uint32_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0u;
+    const uint32_t seq_end = my_chunks * 64u;
+    uint32_t seq_next = 0;  // wave-uniform
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
     // per-lane ray state
     bool has_ray = false;
-    int64_t ray = 0;
-    float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f;
-    float t = 0.f, dist = 0.f, px = 0.f, py = 0.f, pz = 0.f;
+    uint32_t ray = 0;
+    float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
+    float t = 0.f, dist = 0.f;
     int32_t sem = 0, step = 0;
-    const uint32_t* rec = P.records;
-    uint32_t root_slot = 0, n_rec = 0;
-    Box dom{}, lf{}, vd{}, pre{}, cur{};
-    uint32_t lf_slot = 0, pre_rec = 0, cur_rec = 0;
-    int32_t depth = 0;
-    bool lf_ok = false, vd_ok = false, pre_ok = false, fresh = false, descending = false;
+    uint32_t rec_base = 0, root_slot = 0, n_rec = 0;  // this ray's scene
+    Box dom{}, lf{}, vd{}, pre{};
+    uint32_t lf_slot = 0, pre_rec = 0;
+    bool lf_ok = false, vd_ok = false, pre_ok = false;
 
     while (true) {
         // ---- refill lanes without a ray from the wave's chunk sequence ----
         const uint64_t need = __ballot(!has_ray);
         if (need != 0ull && seq_next < seq_end) {
             if (!has_ray) {
-                const int64_t s = seq_next + __popcll(need & lt_mask);
+                const uint32_t s = seq_next + static_cast<uint32_t>(__popcll(need & lt_mask));
                 if (s < seq_end) {
-                    const int64_t q = (wave + (s >> 6) * n_waves) * 64 + (s & 63);
-                    if (q < n_rays) {
+                    const uint32_t q = (wave + (s >> 6) * n_waves) * 64u + (s & 63u);
+                    if (q < P.n_rays) {
                         int32_t env;
                         ray = ray_of(P, q, env);
                         const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
@@ -115,11 +152,14 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                         dx = P.dirs[3 * ray + 0];
                         dy = P.dirs[3 * ray + 1];
                         dz = P.dirs[3 * ray + 2];
+                        rx = 1.0f / dx;  // correctly rounded (IEEE division)
+                        ry = 1.0f / dy;
+                        rz = 1.0f / dz;
                         t = 0.f;
                         dist = 0.f;
                         sem = 0;
                         step = 0;
-                        lf_ok = vd_ok = pre_ok = descending = false;
+                        lf_ok = vd_ok = pre_ok = false;
                         has_ray = true;
                         if (sc < 0 || sc >= P.n_scenes) {
                             // unknown scene: report like a fault, no steps
@@ -129,7 +169,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                             has_ray = false;
                         } else {
                             const navi_relaid_scene d = P.scenes[sc];
-                            rec = P.records + 8 * d.rec_offset;
+                            rec_base = static_cast<uint32_t>(d.rec_offset);
                             root_slot = d.root_slot;
                             n_rec = d.n_records;
                             dom = Box{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
@@ -138,111 +178,126 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                     }
                 }
             }
-            seq_next += __popcll(need);
+            seq_next += static_cast<uint32_t>(__popcll(need));
         }
         if (__ballot(has_ray) == 0ull) {
             if (seq_next >= seq_end) break;
             continue;
         }
 
-        bool resolved = false, stale = false, fault = false;
-        float rd = 0.f;
-        int32_t rs = 0;
+        // ---- start the march step (kernel.cu:260-269, query :108-132) ----
+        // Everything below is written with selects, and the descent loop
+        // touches only cur / cur_rec / depth (plus the prefix save), so the
+        // cache boxes stay in fixed registers.
+        step += has_ray ? 1 : 0;
+        const float px = __builtin_fmaf(t, dx, ox);
+        const float py = __builtin_fmaf(t, dy, oy);
+        const float pz = __builtin_fmaf(t, dz, oz);
+        const bool hit_vd = vd_ok && in_box_strict(px, py, pz, vd);
+        const bool outside = !in_box(px, py, pz, dom);
+        const bool hit_lf = lf_ok && in_box(px, py, pz, lf);
+        const bool use_pre = pre_ok && in_box(px, py, pz, pre);
+        const bool root_leaf = (root_slot & 0x80000000u) != 0u;
+        const bool cached = hit_vd || outside || hit_lf;
+        const bool root_hit = !cached && !use_pre && root_leaf;
+        bool descending = has_ray && !cached && !root_hit;
+        const bool fresh = !use_pre;
+        Box cur;
+        cur.x0 = use_pre ? pre.x0 : dom.x0;
+        cur.y0 = use_pre ? pre.y0 : dom.y0;
+        cur.z0 = use_pre ? pre.z0 : dom.z0;
+        cur.x1 = use_pre ? pre.x1 : dom.x1;
+        cur.y1 = use_pre ? pre.y1 : dom.y1;
+        cur.z1 = use_pre ? pre.z1 : dom.z1;
+        uint32_t cur_rec = use_pre ? pre_rec : root_slot;
+        int32_t depth = use_pre ? kPrefixDepth : 0;
+        uint32_t slot = root_slot;  // a root leaf resolves like a leaf child
+        const bool did_descend = descending;
 
-        // ---- start a march step (kernel.cu:260-269 and query :108-132) ----
-        if (has_ray && !descending) {
-            step += 1;
-            px = __builtin_fmaf(t, dx, ox);
-            py = __builtin_fmaf(t, dy, oy);
-            pz = __builtin_fmaf(t, dz, oz);
-            if (vd_ok && in_box_strict(px, py, pz, vd)) {
-                rd = exit_distance(px, py, pz, dx, dy, dz, vd);
-                resolved = true;
-            } else if (!in_box(px, py, pz, dom)) {
-                rd = kOutsideDomain;
-                resolved = true;
-            } else if (lf_ok && in_box(px, py, pz, lf)) {
-                rd = slot_dist(lf_slot);
-                rs = slot_sem(lf_slot);
-                resolved = true;
-            } else if (pre_ok && in_box(px, py, pz, pre)) {
-                cur = pre;
-                cur_rec = pre_rec;
-                depth = kPrefixDepth;
-                fresh = false;
-                descending = true;
-            } else if (root_slot & 0x80000000u) {  // the root itself is a leaf
-                lf = dom;
-                lf_slot = root_slot;
-                lf_ok = true;
-                rd = slot_dist(lf_slot);
-                rs = slot_sem(lf_slot);
-                resolved = true;
-            } else {
-                cur = dom;
-                cur_rec = root_slot;
-                depth = 0;
-                fresh = true;
-                descending = true;
-            }
-        }
-
-        // ---- one descent level (kernel.cu:136-199) ----
-        if (descending) {
-            if (fresh && depth == kPrefixDepth) {
-                pre = cur;
-                pre_rec = cur_rec;
-                pre_ok = true;
-            }
+        // ---- descend, one 4-byte gather per level (kernel.cu:136-199) ----
+        // A per-lane loop: lanes that found their leaf / void leave it and are
+        // masked off; the wave runs it as long as its deepest descent.
+        while (descending) {
+            const bool save = fresh && depth == kPrefixDepth;  // kernel.cu:154-163
+            pre.x0 = save ? cur.x0 : pre.x0;
+            pre.y0 = save ? cur.y0 : pre.y0;
+            pre.z0 = save ? cur.z0 : pre.z0;
+            pre.x1 = save ? cur.x1 : pre.x1;
+            pre.y1 = save ? cur.y1 : pre.y1;
+            pre.z1 = save ? cur.z1 : pre.z1;
+            pre_rec = save ? cur_rec : pre_rec;
+            pre_ok = pre_ok || save;
             const uint32_t oct = descend_octant(px, py, pz, cur);
             // records come from navi_relayout; the bound keeps a corrupt table in memory
-            const uint32_t slot = cur_rec < n_rec ? rec[8 * cur_rec + oct] : kSlotFault;
-            if (slot == kSlotVoid) {
-                vd = cur;
-                vd_ok = true;
-                rd = exit_distance(px, py, pz, dx, dy, dz, vd);
-                resolved = true;
-                descending = false;
-            } else if (slot == kSlotFault) {
-                fault = true;
-                resolved = true;
-                descending = false;
-            } else if (slot & 0x80000000u) {
-                // the reference examines this child at depth + 1 (< 32 required)
-                if (depth + 1 < kMaxDepth) {
-                    lf = cur;
-                    lf_slot = slot;
-                    lf_ok = true;
-                    rd = slot_dist(slot);
-                    rs = slot_sem(slot);
-                } else {
-                    stale = true;
-                }
-                resolved = true;
-                descending = false;
-            } else {
-                depth += 1;
-                cur_rec = slot;
-                if (depth >= kMaxDepth) {  // 32 levels without leaf or void: stale
-                    stale = true;
-                    resolved = true;
-                    descending = false;
-                }
-            }
+            slot = cur_rec < n_rec ? P.records[8u * (rec_base + cur_rec) + oct] : kSlotFault;
+            depth += 1;
+            const bool internal = slot < kSlotFault;
+            cur_rec = internal ? slot : cur_rec;
+            descending = internal && depth < kMaxDepth;
         }
 
+        // ---- classify the query result and update the caches ----
+        uint32_t kind;
+        if (hit_vd) {
+            kind = kResVoid;
+        } else if (outside) {
+            kind = kResOutside;
+        } else if (hit_lf) {
+            kind = kResLeaf;
+        } else if (slot == kSlotVoid) {
+            kind = kResVoid;
+        } else if (slot == kSlotFault) {
+            kind = kResFault;
+        } else if ((slot & 0x80000000u) && depth < kMaxDepth) {
+            kind = kResLeaf;  // the reference examines the child at `depth` (< 32)
+        } else {
+            kind = kResStale;  // 32 levels without leaf or void
+        }
+        const bool new_void = did_descend && kind == kResVoid;
+        const bool new_leaf = (did_descend || root_hit) && kind == kResLeaf;
+        if (root_hit) cur = dom;
+        vd.x0 = new_void ? cur.x0 : vd.x0;
+        vd.y0 = new_void ? cur.y0 : vd.y0;
+        vd.z0 = new_void ? cur.z0 : vd.z0;
+        vd.x1 = new_void ? cur.x1 : vd.x1;
+        vd.y1 = new_void ? cur.y1 : vd.y1;
+        vd.z1 = new_void ? cur.z1 : vd.z1;
+        vd_ok = vd_ok || new_void;
+        lf.x0 = new_leaf ? cur.x0 : lf.x0;
+        lf.y0 = new_leaf ? cur.y0 : lf.y0;
+        lf.z0 = new_leaf ? cur.z0 : lf.z0;
+        lf.x1 = new_leaf ? cur.x1 : lf.x1;
+        lf.y1 = new_leaf ? cur.y1 : lf.y1;
+        lf.z1 = new_leaf ? cur.z1 : lf.z1;
+        lf_slot = new_leaf ? slot : lf_slot;
+        lf_ok = lf_ok || new_leaf;
+
         // ---- finish the step (kernel.cu:297-308) ----
-        if (resolved) {
+        if (has_ray) {
             bool done = false;
-            if (fault) {
+            if (kind == kResFault) {
                 P.out_d[ray] = __builtin_nanf("");
                 P.out_s[ray] = 0;
                 done = true;
             } else {
-                if (!stale) {
-                    dist = rd;
-                    sem = rs;
-                }
+                if (kind == kResVoid) {
+                    // kernel.cu:54-85 on the void box
+                    float e = kOutsideDomain;
+                    if (dx > kDirEps) e = fminf(e, div_exact(vd.x1 - px, dx, rx));
+                    else if (dx < -kDirEps) e = fminf(e, div_exact(vd.x0 - px, dx, rx));
+                    if (dy > kDirEps) e = fminf(e, div_exact(vd.y1 - py, dy, ry));
+                    else if (dy < -kDirEps) e = fminf(e, div_exact(vd.y0 - py, dy, ry));
+                    if (dz > kDirEps) e = fminf(e, div_exact(vd.z1 - pz, dz, rz));
+                    else if (dz < -kDirEps) e = fminf(e, div_exact(vd.z0 - pz, dz, rz));
+                    dist = fmaxf(e, kVoidAdvanceEps);
+                    sem = 0;
+                } else if (kind == kResLeaf) {
+                    dist = half_to_float(lf_slot & 0xffffu);
+                    sem = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
+                } else if (kind == kResOutside) {
+                    dist = kOutsideDomain;
+                    sem = 0;
+                }  // stale: dist / sem keep the previous step's values
                 if (sem != 0 && dist < P.hit_eps) {
                     P.out_d[ray] = t;
                     P.out_s[ray] = sem;
@@ -266,10 +321,8 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
 
 int g_cu_count = 0;
 
-int launch_relaid(const RelaidParams& base, hipStream_t stream) {
-    RelaidParams P = base;
-    const int64_t n_rays = P.n_envs * P.rays_per_env;
-    P.n_chunks = (n_rays + 63) / 64;
+int launch_relaid(RelaidParams P, hipStream_t stream) {
+    P.n_chunks = (P.n_rays + 63u) / 64u;
     if (g_cu_count == 0) {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
@@ -278,9 +331,8 @@ int launch_relaid(const RelaidParams& base, hipStream_t stream) {
         g_cu_count = cus;
     }
     const int threads = 256;
-    const int64_t waves_wanted = P.n_chunks;
     const int64_t max_blocks = static_cast<int64_t>(g_cu_count) * 8;  // 32 waves per CU
-    int64_t blocks = (waves_wanted + 3) / 4;
+    int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
     if (blocks > max_blocks) blocks = max_blocks;
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, stream, P);
@@ -304,7 +356,11 @@ extern "C" int navi_trace_relaid(const uint32_t* records, const navi_relaid_scen
     if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
     if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
-    if (n_envs * rays_per_env == 0) return NAVI_OK;
+    const int64_t n_rays = n_envs * rays_per_env;
+    if (n_rays == 0) return NAVI_OK;
+    // 32-bit work indexing: every ray index times 3 must fit in uint32
+    if (n_rays > 0x3fffffffLL || rays_per_env > 0x3fffffffLL)
+        return set_error(NAVI_E_ARG, "navi_trace_relaid handles at most 2^30 rays per launch");
     if (!origins || !dirs || !out_distances || !out_semantics)
         return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
     RelaidParams P{};
@@ -313,11 +369,13 @@ extern "C" int navi_trace_relaid(const uint32_t* records, const navi_relaid_scen
     P.n_scenes = n_scenes;
     P.env_scene = env_scene;
     P.env_order = env_order;
-    P.n_envs = n_envs;
-    P.rays_per_env = rays_per_env;
+    P.n_rays = static_cast<uint32_t>(n_rays);
+    P.rays_per_env = static_cast<uint32_t>(rays_per_env);
+    P.div_rays = make_fastdiv(P.rays_per_env);
     P.tile_el = (elevation_bins > 0 && elevation_bins % 8 == 0 && rays_per_env % (8LL * elevation_bins) == 0)
-                    ? elevation_bins
-                    : 0;
+                    ? static_cast<uint32_t>(elevation_bins)
+                    : 0u;
+    P.div_tiles_el = make_fastdiv(P.tile_el ? P.tile_el / 8u : 1u);
     P.origins = origins;
     P.dirs = dirs;
     P.out_d = out_distances;
