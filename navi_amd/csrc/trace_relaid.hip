@@ -100,16 +100,20 @@ __device__ __forceinline__ uint32_t ray_of(const RelaidParams& P, uint32_t q, in
     return static_cast<uint32_t>(env) * P.rays_per_env + r;
 }
 
-// a / b for the exit distance: Markstein-corrected product with r = RN(1/b).
-__device__ __forceinline__ float div_exact(float a, float b, float r) {
-    const float aa = fabsf(a);
-    if (__builtin_expect(aa >= 0x1p-60f && aa <= 0x1p60f && fabsf(b) <= 0x1p20f, 1)) {
-        const float q0 = a * r;
-        const float e = __builtin_fmaf(-q0, b, a);
-        return __builtin_fmaf(e, r, q0);
-    }
-    return a / b;
+// a / b for the exit distance: Markstein-corrected product with r = RN(1/b);
+// equal to the IEEE quotient when div_safe(a, b) (no over/underflow anywhere).
+__device__ __forceinline__ float markstein(float a, float b, float r) {
+    const float q0 = a * r;
+    const float e = __builtin_fmaf(-q0, b, a);
+    return __builtin_fmaf(e, r, q0);
 }
+
+__device__ __forceinline__ bool div_safe(float a, float b) {
+    const float aa = fabsf(a), bb = fabsf(b);
+    return (aa >= 0x1p-60f && aa <= 0x1p60f && bb >= 0x1p-20f && bb <= 0x1p20f) || a == 0.0f;
+}
+
+constexpr uint32_t kRefillMin = 16;
 
 enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
 
@@ -136,8 +140,11 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
 
     while (true) {
         // ---- refill lanes without a ray from the wave's chunk sequence ----
+        // Refill once a quarter of the wave is idle (or all of it): the refill
+        // block costs the whole wave, idle lanes only their own slot.
         const uint64_t need = __ballot(!has_ray);
-        if (need != 0ull && seq_next < seq_end) {
+        const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
+        if ((n_need >= kRefillMin || n_need == 64u) && seq_next < seq_end) {
             if (!has_ray) {
                 const uint32_t s = seq_next + static_cast<uint32_t>(__popcll(need & lt_mask));
                 if (s < seq_end) {
@@ -178,7 +185,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                     }
                 }
             }
-            seq_next += static_cast<uint32_t>(__popcll(need));
+            seq_next += n_need;
         }
         if (__ballot(has_ray) == 0ull) {
             if (seq_next >= seq_end) break;
@@ -237,24 +244,12 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         }
 
         // ---- classify the query result and update the caches ----
-        uint32_t kind;
-        if (hit_vd) {
-            kind = kResVoid;
-        } else if (outside) {
-            kind = kResOutside;
-        } else if (hit_lf) {
-            kind = kResLeaf;
-        } else if (slot == kSlotVoid) {
-            kind = kResVoid;
-        } else if (slot == kSlotFault) {
-            kind = kResFault;
-        } else if ((slot & 0x80000000u) && depth < kMaxDepth) {
-            kind = kResLeaf;  // the reference examines the child at `depth` (< 32)
-        } else {
-            kind = kResStale;  // 32 levels without leaf or void
-        }
-        const bool new_void = did_descend && kind == kResVoid;
-        const bool new_leaf = (did_descend || root_hit) && kind == kResLeaf;
+        const bool leaf_child = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at `depth` < 32
+        const bool is_void = hit_vd || (!cached && slot == kSlotVoid);
+        const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
+        const bool is_fault = !cached && slot == kSlotFault;
+        const bool new_void = did_descend && is_void;
+        const bool new_leaf = !cached && is_leaf;  // descent or root leaf
         if (root_hit) cur = dom;
         vd.x0 = new_void ? cur.x0 : vd.x0;
         vd.y0 = new_void ? cur.y0 : vd.y0;
@@ -273,48 +268,41 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         lf_ok = lf_ok || new_leaf;
 
         // ---- finish the step (kernel.cu:297-308) ----
-        if (has_ray) {
-            bool done = false;
-            if (kind == kResFault) {
-                P.out_d[ray] = __builtin_nanf("");
-                P.out_s[ray] = 0;
-                done = true;
-            } else {
-                if (kind == kResVoid) {
-                    // kernel.cu:54-85 on the void box
-                    float e = kOutsideDomain;
-                    if (dx > kDirEps) e = fminf(e, div_exact(vd.x1 - px, dx, rx));
-                    else if (dx < -kDirEps) e = fminf(e, div_exact(vd.x0 - px, dx, rx));
-                    if (dy > kDirEps) e = fminf(e, div_exact(vd.y1 - py, dy, ry));
-                    else if (dy < -kDirEps) e = fminf(e, div_exact(vd.y0 - py, dy, ry));
-                    if (dz > kDirEps) e = fminf(e, div_exact(vd.z1 - pz, dz, rz));
-                    else if (dz < -kDirEps) e = fminf(e, div_exact(vd.z0 - pz, dz, rz));
-                    dist = fmaxf(e, kVoidAdvanceEps);
-                    sem = 0;
-                } else if (kind == kResLeaf) {
-                    dist = half_to_float(lf_slot & 0xffffu);
-                    sem = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
-                } else if (kind == kResOutside) {
-                    dist = kOutsideDomain;
-                    sem = 0;
-                }  // stale: dist / sem keep the previous step's values
-                if (sem != 0 && dist < P.hit_eps) {
-                    P.out_d[ray] = t;
-                    P.out_s[ray] = sem;
-                    done = true;
-                } else {
-                    t += dist;
-                    if (t > P.max_distance || step >= P.max_steps) {
-                        P.out_d[ray] = t;
-                        P.out_s[ray] = 0;
-                        done = true;
-                    }
-                }
-            }
-            if (done) {
-                if (P.out_steps) P.out_steps[ray] = step;
-                has_ray = false;
-            }
+        // kernel.cu:54-85 on the void box, branch-free: the face per axis is
+        // fixed by the direction's sign; the Markstein quotient is exact unless
+        // an operand is out of its safe range, which takes the IEEE division.
+        const bool ax = dx > kDirEps || dx < -kDirEps;
+        const bool ay = dy > kDirEps || dy < -kDirEps;
+        const bool az = dz > kDirEps || dz < -kDirEps;
+        const float nx = (dx > 0.f ? vd.x1 : vd.x0) - px;
+        const float ny = (dy > 0.f ? vd.y1 : vd.y0) - py;
+        const float nz = (dz > 0.f ? vd.z1 : vd.z0) - pz;
+        float qx = markstein(nx, dx, rx), qy = markstein(ny, dy, ry), qz = markstein(nz, dz, rz);
+        const bool safe = (!ax || div_safe(nx, dx)) && (!ay || div_safe(ny, dy)) && (!az || div_safe(nz, dz));
+        if (!safe && is_void) {
+            qx = nx / dx;
+            qy = ny / dy;
+            qz = nz / dz;
+        }
+        float e = kOutsideDomain;
+        e = ax ? fminf(e, qx) : e;
+        e = ay ? fminf(e, qy) : e;
+        e = az ? fminf(e, qz) : e;
+        const float void_d = fmaxf(e, kVoidAdvanceEps);
+        const float leaf_d = half_to_float(lf_slot & 0xffffu);
+        const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
+        // stale (32 levels without leaf or void): dist / sem keep their values
+        dist = is_void ? void_d : (is_leaf ? leaf_d : (outside ? kOutsideDomain : dist));
+        sem = is_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
+        const bool hit = !is_fault && sem != 0 && dist < P.hit_eps;
+        const float t_next = t + dist;
+        const bool done = has_ray && (is_fault || hit || t_next > P.max_distance || step >= P.max_steps);
+        t = (has_ray && !hit) ? t_next : t;
+        if (done) {
+            P.out_d[ray] = is_fault ? __builtin_nanf("") : t;
+            P.out_s[ray] = hit ? sem : 0;
+            if (P.out_steps) P.out_steps[ray] = step;
+            has_ray = false;
         }
     }
 }
