@@ -91,6 +91,11 @@ def main() -> int:
     ap.add_argument("--cpu-envs", type=int, default=256, help="envs in the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-raw", action="store_true", help="skip timing the reference-layout kernel")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="first run one device copy of this many MiB (known HBM bytes) so a "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run can scale the tracer's counters")
+    ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "trace_relaid_kernel_traffic.json"),
+                    help="measured HBM bytes per launch (written from rocprofv3 --pmc runs)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -118,6 +123,13 @@ def main() -> int:
     origins = np.ascontiguousarray(np.broadcast_to(origins_env[:, None, :], dirs.shape))
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration_mb > 0:
+        n_cal = args.copy_calibration_mb * (1 << 20) // 4
+        src = torch.ones(n_cal, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reads and writes exactly copy_calibration_mb MiB each
+        torch.cuda.synchronize()
+        del src, dst
     res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus], dev)
     t_es = torch.from_numpy(env_scene).to(dev)
     t_o = torch.from_numpy(origins).to(dev)
@@ -210,6 +222,13 @@ def main() -> int:
             "bit_exact_distance": int(np.sum((gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both_nan)),
         }
 
+    traffic = None
+    tp = Path(args.traffic_profile)
+    if tp.exists():
+        prof = json.loads(tp.read_text())
+        if prof.get("workload") == f"{len(corpus)}x{args.resolution}^3/{E}x{R}/{args.max_steps}":
+            traffic = int(prof["hbm_bytes_per_launch"])
+
     line = {
         "metric": "rays/sec on 1 MI355X (256x48 rays/env)",
         "value": round(rays_per_s, 1),
@@ -241,7 +260,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "trace_relaid_kernel",
             "algorithmic_bytes_per_launch": alg_bytes,
         },

@@ -1,0 +1,190 @@
+"""The drop-in boundary without a GPU: the validation contract of
+projects/torch-sdf/torch_sdf/backend.py:28-197 and bindings.cpp:43-110 (messages pinned
+by projects/torch-sdf/tests/test_sphere_tracing.py:294-680), the C ABI library exports,
+and its host-side argument checks. No GPU kernel is launched here.
+"""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from navi_amd import _native, torch_sdf_backend
+from navi_amd.torch_sdf import backend as backend_module
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+class _FakeTensor:
+    def __init__(self, *, shape, dtype, is_cuda=True, contiguous=True):
+        self.shape = shape
+        self.dtype = dtype
+        self.is_cuda = is_cuda
+        self._contiguous = contiguous
+
+    def dim(self):
+        return len(self.shape)
+
+    def size(self, idx):
+        return self.shape[idx]
+
+    def is_contiguous(self):
+        return self._contiguous
+
+
+def _inputs(**over):
+    v = {
+        "dag": _FakeTensor(shape=(8,), dtype=torch.int64),
+        "origins": _FakeTensor(shape=(2, 3, 3), dtype=torch.float32),
+        "dirs": _FakeTensor(shape=(2, 3, 3), dtype=torch.float32),
+        "out_distances": _FakeTensor(shape=(2, 3), dtype=torch.float32),
+        "out_semantics": _FakeTensor(shape=(2, 3), dtype=torch.int32),
+    }
+    v.update(over)
+    return v["dag"], v["origins"], v["dirs"], v["out_distances"], v["out_semantics"]
+
+
+@pytest.fixture
+def fake_gpu(monkeypatch):
+    monkeypatch.setattr(backend_module, "HAS_CUDA_BACKEND", True)
+    monkeypatch.setattr(backend_module, "torch_sdf_backend", object())
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+
+
+def test_native_call_has_eleven_arguments(monkeypatch):
+    captured = {}
+
+    class _Backend:
+        def cast_rays(self, *args, **kw):
+            captured["argc"] = len(args)
+            captured["kw"] = kw
+            captured["max_distance"] = args[6]
+
+    monkeypatch.setattr(backend_module, "HAS_CUDA_BACKEND", True)
+    monkeypatch.setattr(backend_module, "torch_sdf_backend", _Backend())
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    backend_module.cast_rays(*_inputs(), 64, 17.5, [0, 0, 0], [1, 1, 1], 128,
+                             skip_direction_validation=True)
+    assert captured["argc"] == 11 and captured["kw"] == {} and captured["max_distance"] == 17.5
+
+
+@pytest.mark.parametrize("over,args,msg", [
+    ({"dirs": _FakeTensor(shape=(2, 3, 3), dtype=torch.float32, contiguous=False)}, None, "dirs must be contiguous"),
+    ({"dag": _FakeTensor(shape=(8,), dtype=torch.int64, is_cuda=False)}, None, "dag_tensor must be on CUDA"),
+    ({"out_semantics": _FakeTensor(shape=(2, 3), dtype=torch.int32, is_cuda=False)}, None,
+     "out_semantics must be a CUDA tensor"),
+    ({"dirs": _FakeTensor(shape=(2, 3, 3), dtype=torch.float64)}, None, "dirs must have dtype"),
+    ({"out_semantics": _FakeTensor(shape=(2, 4), dtype=torch.int32)}, None, "out_semantics must have shape"),
+    ({}, (0, 30.0, [0, 0, 0], [1, 1, 1], 128), "max_steps must be a positive integer"),
+    ({}, (64, 0.0, [0, 0, 0], [1, 1, 1], 128), "max_distance must be a finite positive float"),
+    ({}, (64, 30.0, [1, 0, 0], [1, 1, 1], 128), r"bbox_min\[0\] must be strictly less than bbox_max\[0\]"),
+    ({}, (64, 30.0, [0.0, float("nan"), 0.0], [1.0, 1.0, 1.0], 128), "must contain only finite floats"),
+    ({}, (64, float("inf"), [0, 0, 0], [1, 1, 1], 128), "max_distance must be a finite positive float"),
+    ({}, (64, 30.0, [0, 0, 0], [1, 1, 1], 0), "resolution must be a positive integer"),
+])
+def test_python_layer_rejections(fake_gpu, over, args, msg):
+    args = args or (64, 30.0, [0, 0, 0], [1, 1, 1], 128)
+    with pytest.raises(RuntimeError, match=msg):
+        backend_module.cast_rays(*_inputs(**over), *args, skip_direction_validation=True)
+
+
+def test_direction_norm_checks():
+    with pytest.raises(RuntimeError, match="normalized within tolerance"):
+        backend_module._validate_direction_norms(torch.tensor([[[1.2, 0.0, 0.0]]]))
+    with pytest.raises(RuntimeError, match="finite direction vectors"):
+        backend_module._validate_direction_norms(torch.tensor([[[float("nan"), 0.0, 1.0]]]))
+    backend_module._validate_direction_norms(torch.tensor([[[1.0, 5e-5, 0.0]]]))
+    with pytest.raises(RuntimeError, match="normalized within tolerance"):
+        torch_sdf_backend._validate_direction_norms(torch.tensor([[[0.5, 0.0, 0.0]]]))
+
+
+def test_no_backend_means_no_fallback(monkeypatch):
+    monkeypatch.setattr(backend_module, "HAS_CUDA_BACKEND", False)
+    with pytest.raises(RuntimeError, match="torch_sdf_backend is not available"):
+        backend_module.cast_rays(*_inputs(), 64, 30.0, [0, 0, 0], [1, 1, 1], 128)
+    monkeypatch.setattr(backend_module, "HAS_CUDA_BACKEND", True)
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError, match="does not support CPU fallback"):
+        backend_module.cast_rays(*_inputs(), 64, 30.0, [0, 0, 0], [1, 1, 1], 128)
+
+
+def test_native_layer_checks_cpu_tensors_before_launch():
+    """bindings.cpp:57-86 order: device first, then contiguity, dtype, shapes, params."""
+    dag = torch.zeros(4, dtype=torch.int64)
+    o = torch.zeros((1, 2, 3))
+    with pytest.raises(RuntimeError, match="dag_tensor must be a CUDA tensor"):
+        torch_sdf_backend.cast_rays(dag, o, o, torch.zeros(1, 2), torch.zeros(1, 2, dtype=torch.int32),
+                                    4, 1.0, [0, 0, 0], [1, 1, 1], 1)
+
+
+def _declared_functions():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[\w]+\s*\**\s*(navi_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_every_declared_symbol_is_exported():
+    import ctypes
+
+    declared = _declared_functions()
+    assert "navi_cast_rays" in declared and "navi_trace_relaid" in declared
+    libs = [ctypes.CDLL(str(ROOT / "navi_amd" / "_lib" / n)) for n in ("libnavi_trace.so", "libnavi_scene.so")]
+    for name in declared:
+        assert any(hasattr(lib, name) for lib in libs), f"{name} declared in include/ but not exported"
+    assert re.fullmatch(r"\d+\.\d+\.\d+", _native.version())
+
+
+def test_c_abi_rejects_bad_arguments_without_a_gpu():
+    lib = _native.lib()
+    f3 = _native.float3
+    code = lib.navi_cast_rays(1, 1, None, None, None, None, 4, 0, 1.0, f3([0, 0, 0]), f3([1, 1, 1]), 1, 0.01,
+                              None, None, None)
+    assert code == _native.NAVI_E_ARG and "max_steps" in _native.last_error()
+    code = lib.navi_cast_rays(1, 1, None, None, None, None, 4, 4, 1.0, f3([1, 0, 0]), f3([1, 1, 1]), 1, 0.01,
+                              None, None, None)
+    assert code == _native.NAVI_E_ARG and "strictly less" in _native.last_error()
+    code = lib.navi_cast_rays(1, 1, None, None, None, None, 0, 4, 1.0, f3([0, 0, 0]), f3([1, 1, 1]), 1, 0.01,
+                              None, None, None)
+    assert code == _native.NAVI_OK  # empty batch: no launch
+    code = lib.navi_trace_relaid(1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
+    assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
+
+
+def test_relayout_on_the_host():
+    """The device record layout answers every point query exactly like the word layout."""
+    import oracle
+    from navi_amd import scenes as S
+
+    scene = S.box_room(resolution=32)
+    words = scene.compile()
+    rec, root, levels = _native.relayout(words)
+    assert root == 0 and levels[0] == 1 and (np.diff(levels) >= 0).all()
+    rng = np.random.default_rng(3)
+    pts = rng.uniform(scene.bbox_min, np.array(scene.bbox_max), (400, 3)).astype(np.float32)
+    ref = oracle.point_query(words, pts, scene.bbox_min_list, scene.bbox_max)
+    for i, p in enumerate(pts):
+        lo = np.array(scene.bbox_min_list, np.float32)
+        hi = np.array(scene.bbox_max, np.float32)
+        slot = root
+        while True:
+            mid = ((lo + hi) * np.float32(0.5)).astype(np.float32)
+            ge = p >= mid
+            o = int(ge[0]) | int(ge[1]) << 1 | int(ge[2]) << 2
+            lo, hi = np.where(ge, mid, lo), np.where(ge, hi, mid)
+            slot = int(rec[slot][o])
+            if slot == 0x7FFFFFFF:
+                assert ref["kind"][i] == 2
+                break
+            if slot >> 31:
+                assert ref["kind"][i] == 1 and ref["semantic"][i] == (slot >> 16) & 0x7FFF
+                assert ref["distance"][i] == np.array([slot & 0xFFFF], np.uint16).view(np.float16)[0]
+                break
+    with pytest.raises(RuntimeError, match="15 bits"):
+        _native.relayout(np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], np.uint64))
