@@ -307,23 +307,28 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
     }
 }
 
-int g_cu_count = 0;
+// Resident waves the chip holds for this kernel: the persistent grid is sized
+// to exactly that, so no wave waits for a slot and the sweep has no second,
+// partly empty round.
+int g_grid_blocks = 0;
 
 int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.n_chunks = (P.n_rays + 63u) / 64u;
-    if (g_cu_count == 0) {
-        int dev = 0, cus = 0;
+    constexpr int kThreads = 256;
+    if (g_grid_blocks == 0) {
+        int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        g_cu_count = cus;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, trace_relaid_kernel, kThreads, 0) != hipSuccess ||
+            per_cu <= 0)
+            per_cu = 4;
+        g_grid_blocks = cus * per_cu;
     }
-    const int threads = 256;
-    const int64_t max_blocks = static_cast<int64_t>(g_cu_count) * 8;  // 32 waves per CU
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
-    if (blocks > max_blocks) blocks = max_blocks;
+    if (blocks > g_grid_blocks) blocks = g_grid_blocks;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), 0, stream, P);
+    hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;
