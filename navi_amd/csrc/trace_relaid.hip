@@ -28,6 +28,10 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <map>
+#include <mutex>
+#include <unordered_map>
+#include <utility>
 
 #include "navi_trace.h"
 #include "trace_common.hpp"
@@ -81,6 +85,8 @@ struct RelaidParams {
     float max_distance;
     float hit_eps;
     uint32_t n_chunks;
+    uint32_t* __restrict__ queue;  // [next unit, finished waves], or null: static schedule
+    uint32_t n_units;              // kUnitRays-ray work units
 };
 
 // Work index q -> ray id (env * R + r).
@@ -114,6 +120,7 @@ __device__ __forceinline__ bool div_safe(float a, float b) {
 }
 
 constexpr uint32_t kRefillMin = 16;
+constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
 
 enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
 
@@ -121,10 +128,13 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
-    // this wave's chunks: wave, wave + n_waves, ...
+    // Static schedule: this wave's chunks are wave, wave + n_waves, ...
     const uint32_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0u;
     const uint32_t seq_end = my_chunks * 64u;
     uint32_t seq_next = 0;  // wave-uniform
+    // Dynamic schedule: units claimed from the queue, `unit_used` rays of `unit` handed out.
+    uint32_t unit = 0, unit_used = kUnitRays;
+    bool exhausted = (P.queue == nullptr) ? (seq_end == 0) : false;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
     // per-lane ray state
@@ -144,51 +154,70 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         // block costs the whole wave, idle lanes only their own slot.
         const uint64_t need = __ballot(!has_ray);
         const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
-        if ((n_need >= kRefillMin || n_need == 64u) && seq_next < seq_end) {
-            if (!has_ray) {
-                const uint32_t s = seq_next + static_cast<uint32_t>(__popcll(need & lt_mask));
-                if (s < seq_end) {
-                    const uint32_t q = (wave + (s >> 6) * n_waves) * 64u + (s & 63u);
-                    if (q < P.n_rays) {
-                        int32_t env;
-                        ray = ray_of(P, q, env);
-                        const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
-                        ox = P.origins[3 * ray + 0];
-                        oy = P.origins[3 * ray + 1];
-                        oz = P.origins[3 * ray + 2];
-                        dx = P.dirs[3 * ray + 0];
-                        dy = P.dirs[3 * ray + 1];
-                        dz = P.dirs[3 * ray + 2];
-                        rx = 1.0f / dx;  // correctly rounded (IEEE division)
-                        ry = 1.0f / dy;
-                        rz = 1.0f / dz;
-                        t = 0.f;
-                        dist = 0.f;
-                        sem = 0;
-                        step = 0;
-                        lf_ok = vd_ok = pre_ok = false;
-                        has_ray = true;
-                        if (sc < 0 || sc >= P.n_scenes) {
-                            // unknown scene: report like a fault, no steps
-                            P.out_d[ray] = __builtin_nanf("");
-                            P.out_s[ray] = 0;
-                            if (P.out_steps) P.out_steps[ray] = 0;
-                            has_ray = false;
-                        } else {
-                            const navi_relaid_scene d = P.scenes[sc];
-                            rec_base = static_cast<uint32_t>(d.rec_offset);
-                            root_slot = d.root_slot;
-                            n_rec = d.n_records;
-                            dom = Box{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
-                                      d.bbox_max[0], d.bbox_max[1], d.bbox_max[2]};
-                        }
+        if ((n_need >= kRefillMin || n_need == 64u) && !exhausted) {
+            const uint32_t rank = static_cast<uint32_t>(__popcll(need & lt_mask));
+            uint32_t q = 0xffffffffu;
+            if (P.queue == nullptr) {
+                const uint32_t sq = seq_next + rank;
+                if (sq < seq_end) q = (wave + (sq >> 6) * n_waves) * 64u + (sq & 63u);
+                seq_next += n_need;
+                exhausted = seq_next >= seq_end;
+            } else {
+                const uint32_t avail = kUnitRays - unit_used;
+                if (rank < avail) q = unit * kUnitRays + unit_used + rank;
+                if (n_need > avail) {
+                    uint32_t claimed = 0;
+                    if (lane == 0) claimed = atomicAdd(P.queue, 1u);
+                    claimed = __shfl(claimed, 0);
+                    if (claimed < P.n_units) {
+                        if (rank >= avail) q = claimed * kUnitRays + (rank - avail);
+                        unit = claimed;
+                        unit_used = n_need - avail;
+                    } else {
+                        exhausted = true;
+                        unit_used = kUnitRays;
                     }
+                } else {
+                    unit_used += n_need;
                 }
             }
-            seq_next += n_need;
+            if (!has_ray && q < P.n_rays) {
+                int32_t env;
+                ray = ray_of(P, q, env);
+                const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
+                ox = P.origins[3 * ray + 0];
+                oy = P.origins[3 * ray + 1];
+                oz = P.origins[3 * ray + 2];
+                dx = P.dirs[3 * ray + 0];
+                dy = P.dirs[3 * ray + 1];
+                dz = P.dirs[3 * ray + 2];
+                rx = 1.0f / dx;  // correctly rounded (IEEE division)
+                ry = 1.0f / dy;
+                rz = 1.0f / dz;
+                t = 0.f;
+                dist = 0.f;
+                sem = 0;
+                step = 0;
+                lf_ok = vd_ok = pre_ok = false;
+                has_ray = true;
+                if (sc < 0 || sc >= P.n_scenes) {
+                    // unknown scene: report like a fault, no steps
+                    P.out_d[ray] = __builtin_nanf("");
+                    P.out_s[ray] = 0;
+                    if (P.out_steps) P.out_steps[ray] = 0;
+                    has_ray = false;
+                } else {
+                    const navi_relaid_scene d = P.scenes[sc];
+                    rec_base = static_cast<uint32_t>(d.rec_offset);
+                    root_slot = d.root_slot;
+                    n_rec = d.n_records;
+                    dom = Box{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
+                              d.bbox_max[0], d.bbox_max[1], d.bbox_max[2]};
+                }
+            }
         }
         if (__ballot(has_ray) == 0ull) {
-            if (seq_next >= seq_end) break;
+            if (exhausted) break;
             continue;
         }
 
@@ -305,6 +334,14 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
             has_ray = false;
         }
     }
+    // The last wave to finish rearms the queue for the next launch on this
+    // stream: every other wave has made its final claim before counting itself.
+    if (P.queue != nullptr && lane == 0) {
+        if (atomicAdd(P.queue + 1, 1u) == n_waves - 1u) {
+            atomicExch(P.queue, 0u);
+            atomicExch(P.queue + 1, 0u);
+        }
+    }
 }
 
 // Resident waves the chip holds for this kernel: the persistent grid is sized
@@ -312,8 +349,45 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
 // partly empty round.
 int g_grid_blocks = 0;
 
+// Work-queue counters, one pair per (device, stream), allocated once per device
+// at its first launch (a 2 KiB device buffer, zeroed then). Launches on one
+// stream run in order, so a pair is never used by two launches at once; the
+// kernel's last wave rearms it. Streams beyond kQueueSlots use the static schedule.
+constexpr int kQueueSlots = 256;
+std::mutex g_queue_mu;
+std::unordered_map<int, uint32_t*> g_queue_mem;
+std::map<std::pair<int, void*>, int> g_queue_slot;
+
+uint32_t* queue_for(hipStream_t stream) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_queue_mu);
+    uint32_t*& mem = g_queue_mem[dev];
+    if (mem == nullptr) {
+        void* p = nullptr;
+        if (hipMalloc(&p, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess) return nullptr;
+        if (hipMemset(p, 0, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess) {
+            (void)hipFree(p);
+            return nullptr;
+        }
+        mem = static_cast<uint32_t*>(p);
+    }
+    const auto key = std::make_pair(dev, static_cast<void*>(stream));
+    auto it = g_queue_slot.find(key);
+    if (it == g_queue_slot.end()) {
+        int used = 0;
+        for (const auto& kv : g_queue_slot)
+            if (kv.first.first == dev) ++used;
+        if (used >= kQueueSlots) return nullptr;
+        it = g_queue_slot.emplace(key, used).first;
+    }
+    return mem + 2 * it->second;
+}
+
 int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.n_chunks = (P.n_rays + 63u) / 64u;
+    P.n_units = (P.n_rays + kUnitRays - 1u) / kUnitRays;
+    P.queue = queue_for(stream);
     constexpr int kThreads = 256;
     if (g_grid_blocks == 0) {
         int dev = 0, cus = 0, per_cu = 0;
