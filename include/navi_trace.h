@@ -91,18 +91,23 @@ int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, in
 int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
                   uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix);
 
-/* One resident scene in the device layout (device memory, 40 bytes). */
+/* One resident scene in the device layout (device memory, 40 bytes). Several
+ * scenes share one record pool: scene records are concatenated and every child
+ * record slot (a slot value below 0x7ffffffe) is rebased to an absolute pool
+ * index by adding the scene's rec_offset; root_slot is rec_offset for an
+ * internal root, or the inlined leaf of a one-leaf DAG. */
 typedef struct navi_relaid_scene {
     uint64_t rec_offset;  /* first record of this scene in the record pool */
     uint32_t n_records;
-    uint32_t root_slot;   /* from navi_relayout */
+    uint32_t root_slot;
     float bbox_min[3];
     float bbox_max[3];
 } navi_relaid_scene;
 
 /*
  * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
- * traces scenes[env_scene ? env_scene[e] : 0]. Per-ray results are identical
+ * traces scenes[env_scene ? env_scene[e] : 0] (at most 1024 scenes; `records`
+ * holds n_records records with absolute child slots, see navi_relaid_scene). Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
  * (optional, a permutation of [0, n_envs)) is the order envs are swept in —
  * pass envs sorted by scene id so resident scenes stream through the caches
@@ -111,7 +116,8 @@ typedef struct navi_relaid_scene {
  * navi_environment/backends/sdfdag_backend.py:205-221) so rays are traced in
  * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
  */
-int navi_trace_relaid(const uint32_t* records, const navi_relaid_scene* scenes, int32_t n_scenes,
+int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                      int32_t n_scenes,
                       const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                       int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                       const float* dirs, float* out_distances, int32_t* out_semantics,

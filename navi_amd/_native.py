@@ -53,7 +53,7 @@ _lib.navi_relayout.restype = ctypes.c_int
 _lib.navi_relayout.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p, _u32p, _vp]
 _lib.navi_trace_relaid.restype = ctypes.c_int
 _lib.navi_trace_relaid.argtypes = [
-    _vp, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, _vp,
+    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, _vp,
     _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 

@@ -67,6 +67,7 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
 
 struct RelaidParams {
     const uint32_t* __restrict__ records;
+    uint32_t n_records;  // records in the pool (child slots are absolute indices)
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
@@ -122,9 +123,25 @@ __device__ __forceinline__ bool div_safe(float a, float b) {
 constexpr uint32_t kRefillMin = 16;
 constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
 
+// A scene as the kernel reads it, staged in LDS once per workgroup so a lane
+// keeps only its scene index in registers.
+struct SceneLds {
+    float x0, y0, z0, x1, y1, z1;
+    uint32_t root;  // absolute record of the root, or the inlined root leaf
+    uint32_t pad;
+};
+constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
+
 enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
 
 __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
+    extern __shared__ SceneLds lds_scenes[];
+    for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
+        const navi_relaid_scene d = P.scenes[i];
+        lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
+                                 d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
+    }
+    __syncthreads();
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
@@ -143,8 +160,8 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
     float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
     float t = 0.f, dist = 0.f;
     int32_t sem = 0, step = 0;
-    uint32_t rec_base = 0, root_slot = 0, n_rec = 0;  // this ray's scene
-    Box dom{}, lf{}, vd{}, pre{};
+    uint32_t scene = 0;  // this ray's scene (an index into lds_scenes)
+    Box lf{}, vd{}, pre{};
     uint32_t lf_slot = 0, pre_rec = 0;
     bool lf_ok = false, vd_ok = false, pre_ok = false;
 
@@ -207,12 +224,17 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                     if (P.out_steps) P.out_steps[ray] = 0;
                     has_ray = false;
                 } else {
-                    const navi_relaid_scene d = P.scenes[sc];
-                    rec_base = static_cast<uint32_t>(d.rec_offset);
-                    root_slot = d.root_slot;
-                    n_rec = d.n_records;
-                    dom = Box{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
-                              d.bbox_max[0], d.bbox_max[1], d.bbox_max[2]};
+                    scene = static_cast<uint32_t>(sc);
+                    // A one-leaf DAG answers every in-domain query with that leaf
+                    // and the domain box (kernel.cu:139-152 at depth 0): prime the
+                    // leaf cache with it, which gives the same results as the
+                    // first query would.
+                    const SceneLds& S = lds_scenes[sc];
+                    if (S.root & 0x80000000u) {
+                        lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                        lf_slot = S.root;
+                        lf_ok = true;
+                    }
                 }
             }
         }
@@ -226,6 +248,8 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         // touches only cur / cur_rec / depth (plus the prefix save), so the
         // cache boxes stay in fixed registers.
         step += has_ray ? 1 : 0;
+        const SceneLds& S = lds_scenes[scene];
+        const Box dom{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
         const float px = __builtin_fmaf(t, dx, ox);
         const float py = __builtin_fmaf(t, dy, oy);
         const float pz = __builtin_fmaf(t, dz, oz);
@@ -233,10 +257,8 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         const bool outside = !in_box(px, py, pz, dom);
         const bool hit_lf = lf_ok && in_box(px, py, pz, lf);
         const bool use_pre = pre_ok && in_box(px, py, pz, pre);
-        const bool root_leaf = (root_slot & 0x80000000u) != 0u;
-        const bool cached = hit_vd || outside || hit_lf;
-        const bool root_hit = !cached && !use_pre && root_leaf;
-        bool descending = has_ray && !cached && !root_hit;
+        const bool cached = hit_vd || outside || hit_lf;  // one-leaf scenes always hit here
+        bool descending = has_ray && !cached;
         const bool fresh = !use_pre;
         Box cur;
         cur.x0 = use_pre ? pre.x0 : dom.x0;
@@ -245,9 +267,9 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         cur.x1 = use_pre ? pre.x1 : dom.x1;
         cur.y1 = use_pre ? pre.y1 : dom.y1;
         cur.z1 = use_pre ? pre.z1 : dom.z1;
-        uint32_t cur_rec = use_pre ? pre_rec : root_slot;
+        uint32_t cur_rec = use_pre ? pre_rec : S.root;
         int32_t depth = use_pre ? kPrefixDepth : 0;
-        uint32_t slot = root_slot;  // a root leaf resolves like a leaf child
+        uint32_t slot = 0;
         const bool did_descend = descending;
 
         // ---- descend, one 4-byte gather per level (kernel.cu:136-199) ----
@@ -265,7 +287,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
             pre_ok = pre_ok || save;
             const uint32_t oct = descend_octant(px, py, pz, cur);
             // records come from navi_relayout; the bound keeps a corrupt table in memory
-            slot = cur_rec < n_rec ? P.records[8u * (rec_base + cur_rec) + oct] : kSlotFault;
+            slot = cur_rec < P.n_records ? P.records[8u * cur_rec + oct] : kSlotFault;
             depth += 1;
             const bool internal = slot < kSlotFault;
             cur_rec = internal ? slot : cur_rec;
@@ -278,8 +300,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
         const bool is_fault = !cached && slot == kSlotFault;
         const bool new_void = did_descend && is_void;
-        const bool new_leaf = !cached && is_leaf;  // descent or root leaf
-        if (root_hit) cur = dom;
+        const bool new_leaf = !cached && is_leaf;  // from a descent
         vd.x0 = new_void ? cur.x0 : vd.x0;
         vd.y0 = new_void ? cur.y0 : vd.y0;
         vd.z0 = new_void ? cur.z0 : vd.z0;
@@ -347,7 +368,8 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
 // Resident waves the chip holds for this kernel: the persistent grid is sized
 // to exactly that, so no wave waits for a slot and the sweep has no second,
 // partly empty round.
-int g_grid_blocks = 0;
+// (per LDS size of the launch; guarded by g_queue_mu).
+std::map<size_t, int> g_grid_blocks;
 
 // Work-queue counters, one pair per (device, stream), allocated once per device
 // at its first launch (a 2 KiB device buffer, zeroed then). Launches on one
@@ -389,20 +411,29 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.n_units = (P.n_rays + kUnitRays - 1u) / kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
-    if (g_grid_blocks == 0) {
+    const size_t lds = static_cast<size_t>(P.n_scenes) * sizeof(SceneLds);
+    int grid_blocks = 0;
+    {
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        auto it = g_grid_blocks.find(lds);
+        if (it != g_grid_blocks.end()) grid_blocks = it->second;
+    }
+    if (grid_blocks == 0) {
         int dev = 0, cus = 0, per_cu = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, trace_relaid_kernel, kThreads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, trace_relaid_kernel, kThreads, lds) != hipSuccess ||
             per_cu <= 0)
             per_cu = 4;
-        g_grid_blocks = cus * per_cu;
+        grid_blocks = cus * per_cu;
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        g_grid_blocks[lds] = grid_blocks;
     }
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
-    if (blocks > g_grid_blocks) blocks = g_grid_blocks;
+    if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, P);
+    hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;
@@ -410,7 +441,8 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
 
 }  // namespace navi
 
-extern "C" int navi_trace_relaid(const uint32_t* records, const navi_relaid_scene* scenes, int32_t n_scenes,
+extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                                 int32_t n_scenes,
                                  const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                                  int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                                  const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -423,6 +455,8 @@ extern "C" int navi_trace_relaid(const uint32_t* records, const navi_relaid_scen
     if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
     if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
+    if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
+    if (n_records >= kSlotFault) return set_error(NAVI_E_ARG, "record pool exceeds 2^31 - 2 records");
     const int64_t n_rays = n_envs * rays_per_env;
     if (n_rays == 0) return NAVI_OK;
     // 32-bit work indexing: every ray index times 3 must fit in uint32
@@ -432,6 +466,7 @@ extern "C" int navi_trace_relaid(const uint32_t* records, const navi_relaid_scen
         return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
     RelaidParams P{};
     P.records = records;
+    P.n_records = static_cast<uint32_t>(n_records);
     P.scenes = scenes;
     P.n_scenes = n_scenes;
     P.env_scene = env_scene;

@@ -69,13 +69,21 @@ class ResidentScenes:
                 break
             rtable[i]["rec_offset"] = roff
             rtable[i]["n_records"] = rec.shape[0]
-            rtable[i]["root_slot"] = root
+            # child record slots become absolute pool indices
+            rec = rec.copy()
+            child = rec < 0x7FFFFFFE
+            rec[child] += np.uint32(roff)
+            rtable[i]["root_slot"] = root if root & 0x80000000 else roff + root
             rtable[i]["bbox_min"] = table[i]["bbox_min"]
             rtable[i]["bbox_max"] = table[i]["bbox_max"]
             recs.append(rec)
             roff += rec.shape[0]
         if self.relaid_ok:
+            if roff + 1 >= 0x7FFFFFFE:
+                self.relaid_ok = False
+        if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
+            self.n_records = int(roff)
             self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)
             self.relaid_table = torch.from_numpy(rtable.view(np.uint8).copy()).to(self.device)
             self.record_counts = [int(r.shape[0]) for r in recs]
@@ -131,7 +139,7 @@ class ResidentScenes:
             with torch.cuda.device(self.device):
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 code = _native.lib().navi_trace_relaid(
-                    self.records.data_ptr(), self.relaid_table.data_ptr(), self.n_scenes,
+                    self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
                     env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
                     int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
                     out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),

@@ -153,7 +153,8 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     code = lib.navi_cast_rays(1, 1, None, None, None, None, 0, 4, 1.0, f3([0, 0, 0]), f3([1, 1, 1]), 1, 0.01,
                               None, None, None)
     assert code == _native.NAVI_OK  # empty batch: no launch
-    code = lib.navi_trace_relaid(1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
+    code = lib.navi_trace_relaid(1, 1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None,
+                                  None)
     assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
 
 
