@@ -286,8 +286,9 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
             pre_rec = save ? cur_rec : pre_rec;
             pre_ok = pre_ok || save;
             const uint32_t oct = descend_octant(px, py, pz, cur);
-            // records come from navi_relayout; the bound keeps a corrupt table in memory
-            slot = cur_rec < P.n_records ? P.records[8u * cur_rec + oct] : kSlotFault;
+            // Child slots from navi_relayout are always in range; the clamp only
+            // keeps a corrupt caller-built pool inside its allocation.
+            slot = P.records[8u * min(cur_rec, P.n_records - 1u) + oct];
             depth += 1;
             const bool internal = slot < kSlotFault;
             cur_rec = internal ? slot : cur_rec;
