@@ -105,9 +105,23 @@ typedef struct navi_relaid_scene {
 } navi_relaid_scene;
 
 /*
+ * Root table of one scene (no reference counterpart; host memory in and out):
+ * 4096 u64 entries, entry o0 << 9 | o1 << 6 | o2 << 3 | o3 (o_l the octant
+ * taken at depth l) = the slot a descent from the root meets within four
+ * levels (bits 31..0: a leaf, void or out-of-range slot, or the record of the
+ * internal node at depth 4) | its depth (bits 34..32; 0 for a one-leaf DAG).
+ * Pass the scene's records and root_slot as the tracer sees them (absolute
+ * record indices in a pool), so record slots in the table are absolute too.
+ */
+int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                          uint64_t* out_table);
+
+/*
  * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
  * traces scenes[env_scene ? env_scene[e] : 0] (at most 1024 scenes; `records`
- * holds n_records records with absolute child slots, see navi_relaid_scene). Per-ray results are identical
+ * holds n_records records with absolute child slots, see navi_relaid_scene;
+ * root_tables holds n_scenes * 4096 entries, scene s at s * 4096, from
+ * navi_build_root_table). Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
  * (optional, a permutation of [0, n_envs)) is the order envs are swept in —
  * pass envs sorted by scene id so resident scenes stream through the caches
@@ -117,7 +131,7 @@ typedef struct navi_relaid_scene {
  * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
  */
 int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                      int32_t n_scenes,
+                      int32_t n_scenes, const uint64_t* root_tables,
                       const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                       int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                       const float* dirs, float* out_distances, int32_t* out_semantics,

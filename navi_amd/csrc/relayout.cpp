@@ -127,3 +127,33 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
     *n_records = queue.size();
     return NAVI_OK;
 }
+
+// Root table: what a descent from the root reaches within the first four
+// levels (kernel.cu:136-199 stops at a leaf or void cell; the prefix cache of
+// kernel.cu:154-163 keys on the internal node met at depth 4). Entry
+// c = o0 << 9 | o1 << 6 | o2 << 3 | o3 (o_l the octant taken at depth l) holds
+// the slot met and, in bits 32..34, its depth d: a leaf / void / fault slot at
+// d <= 4, or the record of the internal node at d = 4. Only octant bits are
+// involved, so a tracer that computes the four splits itself and reads one
+// entry follows the same path as four record reads. A one-leaf DAG maps
+// every entry to its root leaf at depth 0.
+extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                                     uint64_t* out_table) {
+    using navi::set_error;
+    if (!out_table || (!records && n_records)) return set_error(NAVI_E_ARG, "null argument");
+    for (uint32_t c = 0; c < 4096u; ++c) {
+        uint32_t slot = root_slot, d = 0;
+        if (!(root_slot & 0x80000000u)) {
+            uint32_t r = root_slot;
+            for (uint32_t l = 0; l < 4u; ++l) {
+                const uint32_t oct = (c >> (3u * (3u - l))) & 7u;
+                slot = static_cast<uint64_t>(r) < n_records ? records[8ull * r + oct] : kSlotFault;
+                d = l + 1u;
+                if (slot >= kSlotFault || d == 4u) break;
+                r = slot;
+            }
+        }
+        out_table[c] = static_cast<uint64_t>(slot) | (static_cast<uint64_t>(d) << 32);
+    }
+    return NAVI_OK;
+}

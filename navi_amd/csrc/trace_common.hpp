@@ -71,4 +71,14 @@ __device__ __forceinline__ uint32_t descend_octant(float px, float py, float pz,
     return oct;
 }
 
+// One split of descend_octant toward a known octant.
+__device__ __forceinline__ void split_box(Box& cur, uint32_t oct) {
+    const float mx = (cur.x0 + cur.x1) * 0.5f;
+    const float my = (cur.y0 + cur.y1) * 0.5f;
+    const float mz = (cur.z0 + cur.z1) * 0.5f;
+    if (oct & 1u) { cur.x0 = mx; } else { cur.x1 = mx; }
+    if (oct & 2u) { cur.y0 = my; } else { cur.y1 = my; }
+    if (oct & 4u) { cur.z0 = mz; } else { cur.z1 = mz; }
+}
+
 }  // namespace navi

@@ -70,6 +70,7 @@ struct RelaidParams {
     uint32_t n_records;  // records in the pool (child slots are absolute indices)
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
+    const uint64_t* __restrict__ root_table;  // 4096 entries per scene
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
     const int32_t* __restrict__ env_order;  // null: identity
     uint32_t n_rays;
@@ -120,7 +121,8 @@ __device__ __forceinline__ bool div_safe(float a, float b) {
     return (aa >= 0x1p-60f && aa <= 0x1p60f && bb >= 0x1p-20f && bb <= 0x1p20f) || a == 0.0f;
 }
 
-constexpr uint32_t kRefillMin = 16;
+constexpr uint32_t kRefillMin = 8;
+constexpr uint32_t kLeafRun = 2;  // leaf-cache steps taken after a leaf step
 constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
 
 // A scene as the kernel reads it, staged in LDS once per workgroup so a lane
@@ -134,14 +136,20 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 
 enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
 
-__global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
     extern __shared__ SceneLds lds_scenes[];
+    // `nested`: every scene box has coordinates below 2^126 in magnitude, so
+    // lo + hi never overflows, every split plane lies within its box and each
+    // descent box lies within its parent and the domain.
+    int nested = 1;
     for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
         const navi_relaid_scene d = P.scenes[i];
         lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
                                  d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
+        for (int a = 0; a < 3; ++a)
+            nested &= (fabsf(d.bbox_min[a]) < 0x1p126f && fabsf(d.bbox_max[a]) < 0x1p126f) ? 1 : 0;
     }
-    __syncthreads();
+    nested = __syncthreads_and(nested);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
@@ -152,7 +160,6 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
     // Dynamic schedule: units claimed from the queue, `unit_used` rays of `unit` handed out.
     uint32_t unit = 0, unit_used = kUnitRays;
     bool exhausted = (P.queue == nullptr) ? (seq_end == 0) : false;
-    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
 
     // per-lane ray state
     bool has_ray = false;
@@ -167,12 +174,14 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
 
     while (true) {
         // ---- refill lanes without a ray from the wave's chunk sequence ----
-        // Refill once a quarter of the wave is idle (or all of it): the refill
+        // Refill once an eighth of the wave is idle (or all of it): the refill
         // block costs the whole wave, idle lanes only their own slot.
         const uint64_t need = __ballot(!has_ray);
         const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
         if ((n_need >= kRefillMin || n_need == 64u) && !exhausted) {
-            const uint32_t rank = static_cast<uint32_t>(__popcll(need & lt_mask));
+            // idle lanes below this one (mbcnt: set bits of `need` under the lane)
+            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
             uint32_t q = 0xffffffffu;
             if (P.queue == nullptr) {
                 const uint32_t sq = seq_next + rank;
@@ -185,7 +194,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
                 if (n_need > avail) {
                     uint32_t claimed = 0;
                     if (lane == 0) claimed = atomicAdd(P.queue, 1u);
-                    claimed = __shfl(claimed, 0);
+                    claimed = __builtin_amdgcn_readlane(claimed, 0);
                     if (claimed < P.n_units) {
                         if (rank >= avail) q = claimed * kUnitRays + (rank - avail);
                         unit = claimed;
@@ -259,7 +268,7 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         const bool use_pre = pre_ok && in_box(px, py, pz, pre);
         const bool cached = hit_vd || outside || hit_lf;  // one-leaf scenes always hit here
         bool descending = has_ray && !cached;
-        const bool fresh = !use_pre;
+        const bool did_descend = descending;
         Box cur;
         cur.x0 = use_pre ? pre.x0 : dom.x0;
         cur.y0 = use_pre ? pre.y0 : dom.y0;
@@ -267,24 +276,44 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
         cur.x1 = use_pre ? pre.x1 : dom.x1;
         cur.y1 = use_pre ? pre.y1 : dom.y1;
         cur.z1 = use_pre ? pre.z1 : dom.z1;
-        uint32_t cur_rec = use_pre ? pre_rec : S.root;
-        int32_t depth = use_pre ? kPrefixDepth : 0;
+        uint32_t cur_rec = pre_rec;
+        int32_t depth = kPrefixDepth;
         uint32_t slot = 0;
-        const bool did_descend = descending;
 
-        // ---- descend, one 4-byte gather per level (kernel.cu:136-199) ----
+        // ---- a descent from the root: four splits, one root-table read ----
+        // The root table holds what four record reads from the root would
+        // meet (navi_build_root_table); the splits are the descent's own
+        // float operations, so the boxes are the descent's boxes bit for bit.
+        if (descending && !use_pre) {
+            uint32_t cell = 0;
+#pragma unroll
+            for (int l = 0; l < kPrefixDepth; ++l) cell = (cell << 3) | descend_octant(px, py, pz, cur);
+            const uint64_t e = P.root_table[(scene << 12) | cell];
+            slot = static_cast<uint32_t>(e);
+            depth = static_cast<int32_t>(e >> 32);
+            if (depth < kPrefixDepth) {
+                // leaf / void / fault above depth 4 (rare): its box is the one
+                // after `depth` splits
+                cur = dom;
+                for (int32_t l = 0; l < depth; ++l) split_box(cur, (cell >> (3 * (kPrefixDepth - 1 - l))) & 7u);
+            }
+            const bool internal = slot < kSlotFault;  // an internal node at depth 4
+            pre.x0 = internal ? cur.x0 : pre.x0;      // kernel.cu:154-163
+            pre.y0 = internal ? cur.y0 : pre.y0;
+            pre.z0 = internal ? cur.z0 : pre.z0;
+            pre.x1 = internal ? cur.x1 : pre.x1;
+            pre.y1 = internal ? cur.y1 : pre.y1;
+            pre.z1 = internal ? cur.z1 : pre.z1;
+            pre_rec = internal ? slot : pre_rec;
+            pre_ok = pre_ok || internal;
+            cur_rec = slot;
+            descending = internal;
+        }
+
+        // ---- descend below depth 4, one 4-byte gather per level (kernel.cu:136-199) ----
         // A per-lane loop: lanes that found their leaf / void leave it and are
         // masked off; the wave runs it as long as its deepest descent.
         while (descending) {
-            const bool save = fresh && depth == kPrefixDepth;  // kernel.cu:154-163
-            pre.x0 = save ? cur.x0 : pre.x0;
-            pre.y0 = save ? cur.y0 : pre.y0;
-            pre.z0 = save ? cur.z0 : pre.z0;
-            pre.x1 = save ? cur.x1 : pre.x1;
-            pre.y1 = save ? cur.y1 : pre.y1;
-            pre.z1 = save ? cur.z1 : pre.z1;
-            pre_rec = save ? cur_rec : pre_rec;
-            pre_ok = pre_ok || save;
             const uint32_t oct = descend_octant(px, py, pz, cur);
             // Child slots from navi_relayout are always in range; the clamp only
             // keeps a corrupt caller-built pool inside its allocation.
@@ -354,6 +383,42 @@ __global__ __launch_bounds__(256) void trace_relaid_kernel(RelaidParams P) {
             P.out_s[ray] = hit ? sem : 0;
             if (P.out_steps) P.out_steps[ray] = step;
             has_ray = false;
+        }
+
+        // ---- further steps answered by the leaf cache alone ----
+        // After a leaf step that neither hit nor ended the ray, the next point
+        // often stays in the same leaf box; such a step (kernel.cu:260-305
+        // with the void-cache, domain and leaf-cache tests of :265-267 and
+        // :108-118 in that order) repeats the distance and semantic just
+        // used, so it cannot hit. Up to kLeafRun of them are taken here per
+        // lane, far cheaper than a full step; the first point that leaves the
+        // box is left to the next full step, which recomputes it.
+        // With nested boxes the first two tests cannot fire inside the leaf
+        // box: it lies within the domain, and the cached void cell is another
+        // terminal cell of the same tree, so the two differ on a split plane
+        // with the leaf box on its closed side and the void interior strictly
+        // on the other.
+        bool run = has_ray && is_leaf;
+        for (uint32_t k = 0; k < kLeafRun && run; ++k) {
+            const float qx = __builtin_fmaf(t, dx, ox);
+            const float qy = __builtin_fmaf(t, dy, oy);
+            const float qz = __builtin_fmaf(t, dz, oz);
+            run = in_box(qx, qy, qz, lf);
+            if (!nested) {
+                const Box dm{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                run = run && !(vd_ok && in_box_strict(qx, qy, qz, vd)) && in_box(qx, qy, qz, dm);
+            }
+            if (run) {
+                step += 1;
+                t = t + dist;
+                if (t > P.max_distance || step >= P.max_steps) {
+                    P.out_d[ray] = t;
+                    P.out_s[ray] = 0;
+                    if (P.out_steps) P.out_steps[ray] = step;
+                    has_ray = false;
+                    run = false;
+                }
+            }
         }
     }
     // The last wave to finish rearms the queue for the next launch on this
@@ -443,7 +508,7 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
 }  // namespace navi
 
 extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                                 int32_t n_scenes,
+                                 int32_t n_scenes, const uint64_t* root_tables,
                                  const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                                  int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                                  const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -456,6 +521,7 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
     if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
     if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
+    if (!root_tables) return set_error(NAVI_E_ARG, "root_tables is required (navi_build_root_table)");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
     if (n_records >= kSlotFault) return set_error(NAVI_E_ARG, "record pool exceeds 2^31 - 2 records");
     const int64_t n_rays = n_envs * rays_per_env;
@@ -470,6 +536,7 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
     P.n_records = static_cast<uint32_t>(n_records);
     P.scenes = scenes;
     P.n_scenes = n_scenes;
+    P.root_table = root_tables;
     P.env_scene = env_scene;
     P.env_order = env_order;
     P.n_rays = static_cast<uint32_t>(n_rays);

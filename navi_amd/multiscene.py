@@ -83,6 +83,9 @@ class ResidentScenes:
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
+            tables = np.concatenate([_native.root_table(allrec[:roff], int(rtable[i]["root_slot"]))
+                                     for i in range(len(scenes))])
+            self.root_tables = torch.from_numpy(tables.view(np.int64)).to(self.device)
             self.n_records = int(roff)
             self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)
             self.relaid_table = torch.from_numpy(rtable.view(np.uint8).copy()).to(self.device)
@@ -140,6 +143,7 @@ class ResidentScenes:
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 code = _native.lib().navi_trace_relaid(
                     self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
+                    self.root_tables.data_ptr(),
                     env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
                     int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
                     out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),

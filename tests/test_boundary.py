@@ -153,9 +153,11 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     code = lib.navi_cast_rays(1, 1, None, None, None, None, 0, 4, 1.0, f3([0, 0, 0]), f3([1, 1, 1]), 1, 0.01,
                               None, None, None)
     assert code == _native.NAVI_OK  # empty batch: no launch
-    code = lib.navi_trace_relaid(1, 1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None,
-                                  None)
+    code = lib.navi_trace_relaid(1, 1, 1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01,
+                                  None, None)
     assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
+    code = lib.navi_trace_relaid(1, 1, 1, 1, None, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
+    assert code == _native.NAVI_E_ARG and "root_tables" in _native.last_error()
 
 
 def test_relayout_on_the_host():
@@ -189,3 +191,47 @@ def test_relayout_on_the_host():
                 break
     with pytest.raises(RuntimeError, match="15 bits"):
         _native.relayout(np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], np.uint64))
+
+
+def _walk(rec, root, cell):
+    """Four levels of record reads from the root along the octants of `cell`."""
+    if root >> 31:
+        return root, 0
+    r = root
+    for lvl in range(4):
+        oct_ = (cell >> (3 * (3 - lvl))) & 7
+        slot = int(rec[r][oct_]) if r < rec.shape[0] else 0x7FFFFFFE
+        if slot >= 0x7FFFFFFE or lvl == 3:
+            return slot, lvl + 1
+        r = slot
+
+
+@pytest.mark.parametrize("case", ["room", "shallow", "malformed", "one_leaf", "offset"])
+def test_root_table_matches_record_walks(case):
+    from navi_amd import scenes as S
+
+    if case in ("room", "offset"):
+        rec, root, _ = _native.relayout(S.box_room(resolution=32).compile())
+    elif case == "shallow":  # leaves at depth 2: every entry ends above depth 4
+        w = [(0xFF << 55) | 1] + list(range(9, 17)) + [(0xFF << 55) | 17] * 8
+        w += [(1 << 63) | ((i + 1) << 16) | 0x3C00 for i in range(8)]
+        rec, root, _ = _native.relayout(np.array(w, np.uint64))
+    elif case == "malformed":  # child table points past the words: fault slots at depth 1
+        rec, root, _ = _native.relayout(np.array([(0xFF << 55) | 5, 1, 2], np.uint64))
+    else:
+        rec, root, _ = _native.relayout(np.array([(1 << 63) | (3 << 16) | 0x3C00], np.uint64))
+    if case == "offset":  # the scene sits at record 7 of a pool
+        rec = np.concatenate([np.full((7, 8), 0x7FFFFFFF, np.uint32), np.where(rec < 0x7FFFFFFE, rec + 7, rec)])
+        root += 7
+    table = _native.root_table(rec, root)
+    slots = table & 0xFFFFFFFF
+    depths = table >> 32
+    for cell in range(4096):
+        slot, d = _walk(rec, root, cell)
+        assert (int(slots[cell]), int(depths[cell])) == (slot, d), cell
+    if case == "shallow":
+        assert set(depths.tolist()) == {2}
+    if case == "one_leaf":
+        assert set(depths.tolist()) == {0} and set(slots.tolist()) == {root}
+    if case in ("room", "offset"):
+        assert (depths == 4).any() and (slots[depths == 4] < 0x7FFFFFFE).any()

@@ -210,3 +210,28 @@ def test_relayout_rejects_wide_semantics(gpu):
     words = np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], dtype=np.uint64)
     with pytest.raises(RuntimeError, match="15 bits"):
         _native.relayout(words)
+
+
+def test_relaid_huge_domains(gpu, corpus):
+    """Scene boxes with coordinates of 2^126 and more, where split planes can
+    overflow to infinity and boxes stop nesting: the tracer's leaf-run shortcut
+    must fall back to the full cache tests (same batch as an ordinary scene)."""
+    from navi_amd.multiscene import ResidentScenes
+
+    words = corpus[0].words
+    bounds = [corpus[0].bbox_min_list + list(corpus[0].bbox_max),
+              [-3e38, -3e38, -3e38, 3e38, 3e38, 3e38],
+              [1.5e38, 1.5e38, 1.5e38, 3.4e38, 3.4e38, 3.4e38]]
+    res = ResidentScenes([(words, b[:3], b[3:]) for b in bounds])
+    rng = np.random.default_rng(17)
+    n_env, rays = 6, 800
+    env_scene = np.array([0, 1, 2, 1, 2, 0], np.int32)
+    b = np.array(bounds, np.float64)[env_scene]
+    o = rng.uniform(b[:, None, :3], b[:, None, 3:], (n_env, rays, 3)).astype(np.float32)
+    o = np.where(np.isfinite(o), o, 0.0).astype(np.float32)
+    d = rng.normal(size=(n_env, rays, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    for max_steps, max_distance in ((40, 3e38), (200, 30.0)):
+        ref = _oracle_multi([words] * 3, bounds, env_scene, o, d, max_steps, max_distance)
+        _compare(_run(res, env_scene, o, d, max_steps, max_distance), ref, max_distance,
+                 f"huge/{max_steps}")
