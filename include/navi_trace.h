@@ -91,7 +91,7 @@ int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, in
 int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
                   uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix);
 
-/* One resident scene in the device layout (device memory, 40 bytes). Several
+/* One resident scene in the device layout (device memory, 48 bytes). Several
  * scenes share one record pool: scene records are concatenated and every child
  * record slot (a slot value below 0x7ffffffe) is rebased to an absolute pool
  * index by adding the scene's rec_offset; root_slot is rec_offset for an
@@ -102,7 +102,18 @@ typedef struct navi_relaid_scene {
     uint32_t root_slot;
     float bbox_min[3];
     float bbox_max[3];
+    uint32_t max_depth;   /* navi_record_depth of the scene; 0xffffffff if unknown */
+    uint32_t reserved;    /* 0 */
 } navi_relaid_scene;
+
+/*
+ * Depth of a scene's record graph (no reference counterpart; host memory):
+ * the longest chain of internal records below root_slot (the root at depth
+ * 0), or 0xffffffff when a cycle or an out-of-range record is reachable.
+ * When every scene of a launch has max_depth <= 30 the tracer drops the
+ * 32-level descent limit of kernel.cu:136, which such scenes never reach.
+ */
+int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root_slot, uint32_t* max_depth);
 
 /*
  * Root table of one scene (no reference counterpart; host memory in and out):

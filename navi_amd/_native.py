@@ -54,14 +54,17 @@ _lib.navi_relayout.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p
 _lib.navi_trace_relaid.restype = ctypes.c_int
 _lib.navi_build_root_table.restype = ctypes.c_int
 _lib.navi_build_root_table.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _vp]
+_lib.navi_record_depth.restype = ctypes.c_int
+_lib.navi_record_depth.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _u32p]
 _lib.navi_trace_relaid.argtypes = [
     _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, _vp,
     _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 
-# Layout of navi_relaid_scene (include/navi_trace.h), 40 bytes.
+# Layout of navi_relaid_scene (include/navi_trace.h), 48 bytes.
 RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot", "<u4"),
-                      ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,))]
+                      ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,)), ("max_depth", "<u4"),
+                      ("reserved", "<u4")]
 
 
 def relayout(words):
@@ -91,6 +94,17 @@ def root_table(records, root_slot):
     check(_lib.navi_build_root_table(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
                                      out.ctypes.data))
     return out
+
+
+def record_depth(records, root_slot):
+    """Longest record chain below ``root_slot`` (``navi_record_depth``); 0xffffffff on a cycle."""
+    import numpy as np
+
+    rec = np.ascontiguousarray(records, dtype=np.uint32).reshape(-1, 8)
+    out = ctypes.c_uint32()
+    check(_lib.navi_record_depth(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
+                                 ctypes.byref(out)))
+    return int(out.value)
 
 
 # Layout of navi_scene_desc (include/navi_trace.h), 40 bytes.

@@ -157,3 +157,64 @@ extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records
     }
     return NAVI_OK;
 }
+
+// Longest chain of internal records below the root, in levels: the deepest
+// record reachable from root_slot sits at that depth (the root at 0). Records
+// hold record slots as indices into `records` (a pool). *max_depth is
+// 0xffffffff when a cycle or an out-of-range record is reachable, where the
+// descent limit of kernel.cu:136 decides results. Iterative depth-first
+// search, O(records + slots).
+extern "C" int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                                 uint32_t* max_depth) {
+    using navi::set_error;
+    if (!max_depth || (!records && n_records)) return set_error(NAVI_E_ARG, "null argument");
+    if (root_slot >= kSlotFault) {  // one-leaf DAG (or a void / fault root slot)
+        *max_depth = 0;
+        return NAVI_OK;
+    }
+    if (root_slot >= n_records) {
+        *max_depth = 0xffffffffu;
+        return NAVI_OK;
+    }
+    // height[r]: longest chain of records below r (0 = no internal child);
+    // kOpen marks a record on the current path (a revisit means a cycle).
+    constexpr uint32_t kUnseen = 0xffffffffu, kOpen = 0xfffffffeu;
+    std::vector<uint32_t> height(n_records, kUnseen);
+    struct Frame {
+        uint32_t rec;
+        uint32_t next;  // next octant to visit
+        uint32_t best;
+    };
+    std::vector<Frame> stack;
+    stack.push_back({root_slot, 0u, 0u});
+    height[root_slot] = kOpen;
+    while (!stack.empty()) {
+        Frame& f = stack.back();
+        if (f.next == 8u) {
+            height[f.rec] = f.best;
+            const uint32_t h = f.best;
+            stack.pop_back();
+            if (!stack.empty() && h + 1u > stack.back().best) stack.back().best = h + 1u;
+            continue;
+        }
+        const uint32_t slot = records[8ull * f.rec + f.next++];
+        if (slot >= kSlotFault) continue;  // leaf, void or fault slot
+        if (slot >= n_records) {
+            *max_depth = 0xffffffffu;
+            return NAVI_OK;
+        }
+        const uint32_t h = height[slot];
+        if (h == kOpen) {
+            *max_depth = 0xffffffffu;
+            return NAVI_OK;
+        }
+        if (h == kUnseen) {
+            height[slot] = kOpen;
+            stack.push_back({slot, 0u, 0u});
+        } else if (h + 1u > f.best) {
+            f.best = h + 1u;
+        }
+    }
+    *max_depth = height[root_slot];
+    return NAVI_OK;
+}

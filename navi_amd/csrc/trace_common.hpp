@@ -71,6 +71,24 @@ __device__ __forceinline__ uint32_t descend_octant(float px, float py, float pz,
     return oct;
 }
 
+// descend_octant fused with slot addressing: returns base * 8 + octant, the
+// octant's z, y and x bits appended in that order (one add-with-carry each).
+__device__ __forceinline__ uint32_t descend_index(float px, float py, float pz, Box& cur, uint32_t base) {
+    const float mx = (cur.x0 + cur.x1) * 0.5f;
+    const float my = (cur.y0 + cur.y1) * 0.5f;
+    const float mz = (cur.z0 + cur.z1) * 0.5f;
+    const bool gx = px >= mx, gy = py >= my, gz = pz >= mz;
+    cur.x0 = gx ? mx : cur.x0;
+    cur.x1 = gx ? cur.x1 : mx;
+    cur.y0 = gy ? my : cur.y0;
+    cur.y1 = gy ? cur.y1 : my;
+    cur.z0 = gz ? mz : cur.z0;
+    cur.z1 = gz ? cur.z1 : mz;
+    uint32_t i = base * 2u + (gz ? 1u : 0u);
+    i = i * 2u + (gy ? 1u : 0u);
+    return i * 2u + (gx ? 1u : 0u);
+}
+
 // One split of descend_octant toward a known octant.
 __device__ __forceinline__ void split_box(Box& cur, uint32_t oct) {
     const float mx = (cur.x0 + cur.x1) * 0.5f;

@@ -65,6 +65,8 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
     return (t + ((n - t) >> 1)) >> (f.l - 1);
 }
 
+static_assert(sizeof(navi_relaid_scene) == 48, "navi_relaid_scene is 48 bytes");
+
 struct RelaidParams {
     const uint32_t* __restrict__ records;
     uint32_t n_records;  // records in the pool (child slots are absolute indices)
@@ -141,15 +143,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     // `nested`: every scene box has coordinates below 2^126 in magnitude, so
     // lo + hi never overflows, every split plane lies within its box and each
     // descent box lies within its parent and the domain.
-    int nested = 1;
+    // `shallow`: no record of any scene lies deeper than 30 levels, so every
+    // slot a descent reads is at depth <= 31 and the 32-level limit of
+    // kernel.cu:136 never applies.
+    int nested = 1, shallow = 1;
     for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
         const navi_relaid_scene d = P.scenes[i];
         lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
                                  d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
         for (int a = 0; a < 3; ++a)
             nested &= (fabsf(d.bbox_min[a]) < 0x1p126f && fabsf(d.bbox_max[a]) < 0x1p126f) ? 1 : 0;
+        shallow &= d.max_depth <= static_cast<uint32_t>(kMaxDepth - 2) ? 1 : 0;
     }
     nested = __syncthreads_and(nested);
+    shallow = __syncthreads_and(shallow);
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
@@ -285,10 +292,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // meet (navi_build_root_table); the splits are the descent's own
         // float operations, so the boxes are the descent's boxes bit for bit.
         if (descending && !use_pre) {
-            uint32_t cell = 0;
+            uint32_t cell = scene;  // becomes scene * 4096 + the four octants
 #pragma unroll
-            for (int l = 0; l < kPrefixDepth; ++l) cell = (cell << 3) | descend_octant(px, py, pz, cur);
-            const uint64_t e = P.root_table[(scene << 12) | cell];
+            for (int l = 0; l < kPrefixDepth; ++l) cell = descend_index(px, py, pz, cur, cell);
+            const uint64_t e = P.root_table[cell];
             slot = static_cast<uint32_t>(e);
             depth = static_cast<int32_t>(e >> 32);
             if (depth < kPrefixDepth) {
@@ -313,19 +320,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // ---- descend below depth 4, one 4-byte gather per level (kernel.cu:136-199) ----
         // A per-lane loop: lanes that found their leaf / void leave it and are
         // masked off; the wave runs it as long as its deepest descent.
-        while (descending) {
-            const uint32_t oct = descend_octant(px, py, pz, cur);
-            // Child slots from navi_relayout are always in range; the clamp only
-            // keeps a corrupt caller-built pool inside its allocation.
-            slot = P.records[8u * min(cur_rec, P.n_records - 1u) + oct];
-            depth += 1;
-            const bool internal = slot < kSlotFault;
-            cur_rec = internal ? slot : cur_rec;
-            descending = internal && depth < kMaxDepth;
+        // Child slots from navi_relayout are always in range; the clamp only
+        // keeps a corrupt caller-built pool inside its allocation.
+        if (shallow) {
+            while (descending) {
+                slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
+                cur_rec = slot;  // read again only while internal
+                descending = slot < kSlotFault;
+            }
+        } else {
+            while (descending) {
+                slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
+                depth += 1;
+                cur_rec = slot;
+                descending = slot < kSlotFault && depth < kMaxDepth;
+            }
         }
 
         // ---- classify the query result and update the caches ----
-        const bool leaf_child = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at `depth` < 32
+        const bool leaf_child = (slot & 0x80000000u) != 0u && (shallow || depth < kMaxDepth);  // examined at depth < 32
         const bool is_void = hit_vd || (!cached && slot == kSlotVoid);
         const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
         const bool is_fault = !cached && slot == kSlotFault;
@@ -523,7 +536,8 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
     if (!root_tables) return set_error(NAVI_E_ARG, "root_tables is required (navi_build_root_table)");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
-    if (n_records >= kSlotFault) return set_error(NAVI_E_ARG, "record pool exceeds 2^31 - 2 records");
+    // 32-bit slot addressing: record * 8 + octant must fit in uint32
+    if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
     const int64_t n_rays = n_envs * rays_per_env;
     if (n_rays == 0) return NAVI_OK;
     // 32-bit work indexing: every ray index times 3 must fit in uint32

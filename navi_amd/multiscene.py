@@ -79,12 +79,14 @@ class ResidentScenes:
             recs.append(rec)
             roff += rec.shape[0]
         if self.relaid_ok:
-            if roff + 1 >= 0x7FFFFFFE:
+            if roff > (1 << 29):  # navi_trace_relaid addresses slots with 32-bit record * 8 + octant
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
             tables = np.concatenate([_native.root_table(allrec[:roff], int(rtable[i]["root_slot"]))
                                      for i in range(len(scenes))])
+            for i in range(len(scenes)):
+                rtable[i]["max_depth"] = _native.record_depth(allrec[:roff], int(rtable[i]["root_slot"]))
             self.root_tables = torch.from_numpy(tables.view(np.int64)).to(self.device)
             self.n_records = int(roff)
             self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)

@@ -235,3 +235,67 @@ def test_root_table_matches_record_walks(case):
         assert set(depths.tolist()) == {0} and set(slots.tolist()) == {root}
     if case in ("room", "offset"):
         assert (depths == 4).any() and (slots[depths == 4] < 0x7FFFFFFE).any()
+
+
+def _longest_chain(rec, root):
+    """Brute force: longest record chain below root, None on a cycle."""
+    import functools
+    import sys
+
+    sys.setrecursionlimit(10000)
+    on_path = set()
+
+    @functools.lru_cache(maxsize=None)
+    def h(r):
+        if r in on_path:
+            raise RecursionError
+        on_path.add(r)
+        best = 0
+        for s in rec[r]:
+            s = int(s)
+            if s < 0x7FFFFFFE:
+                best = max(best, h(s) + 1)
+        on_path.discard(r)
+        return best
+
+    try:
+        return h(root)
+    except RecursionError:
+        return None
+
+
+def _chain_words(n):
+    """A chain of n internal nodes, each with one child in octant 7, ending in a leaf."""
+    w = []
+    for i in range(n):
+        w += [(1 << 62) | (2 * i + 1), 2 * i + 2]
+    w[-1] = len(w)
+    return np.array(w + [(1 << 63) | (5 << 16) | 0x3C00], np.uint64)
+
+
+@pytest.mark.parametrize("case", ["room", "chain31", "chain32", "shared", "cycle", "one_leaf"])
+def test_record_depth(case):
+    from navi_amd import scenes as S
+
+    if case == "room":
+        words = S.box_room(resolution=64).compile()
+    elif case.startswith("chain"):
+        words = _chain_words(int(case[5:]))
+    elif case == "shared":  # a DAG whose shared child is reached at depths 1 and 2
+        words = np.array([(0x03 << 55) | 1, 3, 4, (0x01 << 55) | 5, (0x01 << 55) | 6, 4, (1 << 63) | 0x3C00],
+                         np.uint64)
+    elif case == "cycle":
+        words = np.array([(0xFF << 55) | 1] + [0] * 8, np.uint64)
+    else:
+        words = np.array([(1 << 63) | 0x3C00], np.uint64)
+    rec, root, _ = _native.relayout(words)
+    got = _native.record_depth(rec, root)
+    if case == "one_leaf":
+        assert got == 0
+        return
+    want = _longest_chain(rec, root)
+    assert got == (0xFFFFFFFF if want is None else want)
+    if case.startswith("chain"):
+        assert got == int(case[5:]) - 1
+    if case == "shared":
+        assert got == 2

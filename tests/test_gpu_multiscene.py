@@ -235,3 +235,27 @@ def test_relaid_huge_domains(gpu, corpus):
         ref = _oracle_multi([words] * 3, bounds, env_scene, o, d, max_steps, max_distance)
         _compare(_run(res, env_scene, o, d, max_steps, max_distance), ref, max_distance,
                  f"huge/{max_steps}")
+
+
+def test_relaid_descent_limit_chains(gpu, corpus):
+    """Chains of 31 and 33 nested nodes toward the (1, 1, 1) corner: the first
+    keeps every slot above depth 32, the second reaches the 32-level limit
+    (stale results). Batched alone and together, so both descent loops run."""
+    from navi_amd.multiscene import ResidentScenes
+    from tests.test_boundary import _chain_words
+
+    chains = [_chain_words(31), _chain_words(33)]
+    rng = np.random.default_rng(5)
+    rays = 256
+    one = np.float32(1.0)
+    near = one - np.arange(4, dtype=np.float32) * np.float32(2.0 ** -24)
+    o = rng.choice(near, size=(2, rays, 3)).astype(np.float32)
+    o[:, rays // 2:] = rng.uniform(0.0, 1.0, (2, rays // 2, 3)).astype(np.float32)
+    d = rng.normal(size=(2, rays, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    for picks in ([0], [1], [0, 1]):
+        scenes = [(chains[i], [0, 0, 0], [1, 1, 1]) for i in picks]
+        res = ResidentScenes(scenes)
+        env_scene = np.array([0, len(picks) - 1], np.int32)
+        ref = _oracle_multi([s[0] for s in scenes], [[0, 0, 0, 1, 1, 1]] * len(picks), env_scene, o, d, 12, 4.0)
+        _compare(_run(res, env_scene, o, d, 12, 4.0), ref, 4.0, f"chains/{picks}")
