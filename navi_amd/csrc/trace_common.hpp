@@ -71,6 +71,16 @@ __device__ __forceinline__ uint32_t descend_octant(float px, float py, float pz,
     return oct;
 }
 
+// i * 2 + b in one add-with-carry, the comparison's lane mask as carry-in
+// (the compiler spends two operations, a select and a shift-or).
+__device__ __forceinline__ uint32_t append_bit(uint32_t i, bool b) {
+    const uint64_t mask = __ballot(b);  // this lane's bit is b; inactive lanes are ignored
+    uint32_t r;
+    uint64_t carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(i), "s"(mask));
+    return r;
+}
+
 // descend_octant fused with slot addressing: returns base * 8 + octant, the
 // octant's z, y and x bits appended in that order (one add-with-carry each).
 __device__ __forceinline__ uint32_t descend_index(float px, float py, float pz, Box& cur, uint32_t base) {
@@ -84,9 +94,9 @@ __device__ __forceinline__ uint32_t descend_index(float px, float py, float pz, 
     cur.y1 = gy ? cur.y1 : my;
     cur.z0 = gz ? mz : cur.z0;
     cur.z1 = gz ? cur.z1 : mz;
-    uint32_t i = base * 2u + (gz ? 1u : 0u);
-    i = i * 2u + (gy ? 1u : 0u);
-    return i * 2u + (gx ? 1u : 0u);
+    uint32_t i = append_bit(base, gz);
+    i = append_bit(i, gy);
+    return append_bit(i, gx);
 }
 
 // One split of descend_octant toward a known octant.
