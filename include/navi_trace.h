@@ -117,12 +117,14 @@ int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root
 
 /*
  * Root table of one scene (no reference counterpart; host memory in and out):
- * 4096 u64 entries, entry o0 << 9 | o1 << 6 | o2 << 3 | o3 (o_l the octant
- * taken at depth l) = the slot a descent from the root meets within four
- * levels (bits 31..0: a leaf, void or out-of-range slot, or the record of the
- * internal node at depth 4) | its depth (bits 34..32; 0 for a one-leaf DAG).
- * Pass the scene's records and root_slot as the tracer sees them (absolute
- * record indices in a pool), so record slots in the table are absolute too.
+ * 4096 u64 entries over the 16 x 16 x 16 grid of depth-4 cells. Entry
+ * (iz * 16 + iy) * 16 + ix (the cell whose octant at depth l has x bit
+ * (ix >> (3 - l)) & 1, y and z likewise) = the slot a descent from the root
+ * meets within four levels (bits 31..0: a leaf, void or out-of-range slot, or
+ * the record of the internal node at depth 4) | its depth (bits 34..32; 0 for
+ * a one-leaf DAG). Pass the scene's records and root_slot as the tracer sees
+ * them (absolute record indices in a pool), so record slots in the table are
+ * absolute too.
  */
 int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
                           uint64_t* out_table);

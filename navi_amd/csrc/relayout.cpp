@@ -130,13 +130,14 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
 
 // Root table: what a descent from the root reaches within the first four
 // levels (kernel.cu:136-199 stops at a leaf or void cell; the prefix cache of
-// kernel.cu:154-163 keys on the internal node met at depth 4). Entry
-// c = o0 << 9 | o1 << 6 | o2 << 3 | o3 (o_l the octant taken at depth l) holds
-// the slot met and, in bits 32..34, its depth d: a leaf / void / fault slot at
-// d <= 4, or the record of the internal node at d = 4. Only octant bits are
-// involved, so a tracer that computes the four splits itself and reads one
-// entry follows the same path as four record reads. A one-leaf DAG maps
-// every entry to its root leaf at depth 0.
+// kernel.cu:154-163 keys on the internal node met at depth 4). The depth-4
+// cells form a 16 x 16 x 16 grid; entry (iz * 16 + iy) * 16 + ix holds, for
+// the cell whose octant at depth l has x bit (ix >> (3 - l)) & 1 (y, z
+// likewise), the slot met and, in bits 32..34, its depth d: a leaf / void /
+// fault slot at d <= 4, or the record of the internal node at d = 4. Only
+// octant bits are involved, so a tracer that locates the cell itself and
+// reads one entry follows the same path as four record reads. A one-leaf DAG
+// maps every entry to its root leaf at depth 0.
 extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
                                      uint64_t* out_table) {
     using navi::set_error;
@@ -146,7 +147,8 @@ extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records
         if (!(root_slot & 0x80000000u)) {
             uint32_t r = root_slot;
             for (uint32_t l = 0; l < 4u; ++l) {
-                const uint32_t oct = (c >> (3u * (3u - l))) & 7u;
+                const uint32_t b = 3u - l;
+                const uint32_t oct = ((c >> b) & 1u) | (((c >> (4u + b)) & 1u) << 1) | (((c >> (8u + b)) & 1u) << 2);
                 slot = static_cast<uint64_t>(r) < n_records ? records[8ull * r + oct] : kSlotFault;
                 d = l + 1u;
                 if (slot >= kSlotFault || d == 4u) break;

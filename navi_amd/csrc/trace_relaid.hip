@@ -135,11 +135,54 @@ struct SceneLds {
     uint32_t pad;
 };
 constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
+// Split planes of the first four levels, per scene and axis: the 17 planes
+// P_0 = lo, ..., P_16 = hi of the 16 depth-4 cells, then 16 / (hi - lo).
+constexpr int32_t kPlaneStride = 18;
+constexpr int32_t kPlaneScenes = 64;  // launches with more scenes skip the planes (LDS budget)
 
-enum : uint32_t { kResVoid = 0, kResLeaf = 1, kResOutside = 2, kResStale = 3, kResFault = 4 };
+// Split planes of one axis, nested midpoints computed with the descent's own
+// operations (kernel.cu:165-176), so cell boxes are the descent's boxes bit
+// for bit. Returns whether they support the direct cell lookup of
+// plane_cell: finite, each within 0.2 cell of the uniform grid, and an
+// accurate scale.
+__device__ bool make_planes(float lo, float hi, float* out) {
+    float pl[17];
+    pl[0] = lo;
+    pl[16] = hi;
+    for (int step = 16; step > 1; step >>= 1)
+        for (int k = 0; k < 16; k += step) pl[k + step / 2] = (pl[k] + pl[k + step]) * 0.5f;
+    const float w = hi - lo;
+    const float scale = 16.0f / w;
+    const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / 16.0;
+    bool ok = w > 0.0f && w <= 0x1p127f && scale > 0.0f && scale <= 0x1p127f && cw > 0.0 &&
+              fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6;
+    for (int k = 0; k <= 16; ++k) {
+        ok = ok && fabs(static_cast<double>(pl[k]) - (static_cast<double>(lo) + k * cw)) <= 0.2 * cw;
+        out[k] = pl[k];
+    }
+    out[16 + 1] = scale;
+    return ok;
+}
 
+// Depth-4 cell of p along one axis from its planes, and the cell's bounds.
+// With planes within 0.2 cell of uniform, u = (p - P_0) * scale - 0.25 lies
+// within (j - 0.46, j + 0.96) for the cell j that holds p (P_j <= p < P_j+1,
+// or j = 15 at p = P_16), so trunc(u) is j - 1 or j (0 when u < 0, where j is
+// 0); one comparison with the next plane settles it.
+__device__ __forceinline__ uint32_t plane_cell(float p, const float* pl, float& lo, float& hi) {
+    const float u = __builtin_fmaf(p - pl[0], pl[16 + 1], -0.25f);
+    const uint32_t j0 = static_cast<uint32_t>(static_cast<int32_t>(u));
+    const float a = pl[j0], b = pl[j0 + 1], c = pl[j0 + 2];  // pl[17] is read (unused) at j0 = 15
+    const bool up = p >= b && j0 < 15u;
+    lo = up ? b : a;
+    hi = up ? c : b;
+    return j0 + (up ? 1u : 0u);
+}
+
+template <bool kPlanes>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
     extern __shared__ SceneLds lds_scenes[];
+    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
     // `nested`: every scene box has coordinates below 2^126 in magnitude, so
     // lo + hi never overflows, every split plane lies within its box and each
     // descent box lies within its parent and the domain.
@@ -157,6 +200,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     }
     nested = __syncthreads_and(nested);
     shallow = __syncthreads_and(shallow);
+    // `planes`: every scene's depth-4 cells can be located from its planes
+    int planes = kPlanes ? 1 : 0;
+    if (kPlanes) {
+        for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
+            const navi_relaid_scene& d = P.scenes[i / 3];
+            const int a = i % 3;
+            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], lds_planes + i * kPlaneStride) ? 1 : 0;
+        }
+        planes = __syncthreads_and(planes);
+    }
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
@@ -287,22 +340,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         int32_t depth = kPrefixDepth;
         uint32_t slot = 0;
 
-        // ---- a descent from the root: four splits, one root-table read ----
+        // ---- a descent from the root: locate the depth-4 cell, one root-table read ----
         // The root table holds what four record reads from the root would
-        // meet (navi_build_root_table); the splits are the descent's own
-        // float operations, so the boxes are the descent's boxes bit for bit.
+        // meet (navi_build_root_table). The cell comes from the split planes
+        // when the scenes allow it, else from four splits done here; either
+        // way its box is the descent's box bit for bit.
         if (descending && !use_pre) {
-            uint32_t cell = scene;  // becomes scene * 4096 + the four octants
+            uint32_t jx = 0, jy = 0, jz = 0;
+            const float* pl = lds_planes + scene * (3 * kPlaneStride);
+            if (kPlanes && planes) {
+                jx = plane_cell(px, pl, cur.x0, cur.x1);
+                jy = plane_cell(py, pl + kPlaneStride, cur.y0, cur.y1);
+                jz = plane_cell(pz, pl + 2 * kPlaneStride, cur.z0, cur.z1);
+            } else {
 #pragma unroll
-            for (int l = 0; l < kPrefixDepth; ++l) cell = descend_index(px, py, pz, cur, cell);
-            const uint64_t e = P.root_table[cell];
+                for (int l = 0; l < kPrefixDepth; ++l) {
+                    const float mx = (cur.x0 + cur.x1) * 0.5f;
+                    const float my = (cur.y0 + cur.y1) * 0.5f;
+                    const float mz = (cur.z0 + cur.z1) * 0.5f;
+                    const bool gx = px >= mx, gy = py >= my, gz = pz >= mz;
+                    cur.x0 = gx ? mx : cur.x0;
+                    cur.x1 = gx ? cur.x1 : mx;
+                    cur.y0 = gy ? my : cur.y0;
+                    cur.y1 = gy ? cur.y1 : my;
+                    cur.z0 = gz ? mz : cur.z0;
+                    cur.z1 = gz ? cur.z1 : mz;
+                    jx = append_bit(jx, gx);
+                    jy = append_bit(jy, gy);
+                    jz = append_bit(jz, gz);
+                }
+            }
+            const uint64_t e = P.root_table[(((scene << 4 | jz) << 4 | jy) << 4) | jx];
             slot = static_cast<uint32_t>(e);
             depth = static_cast<int32_t>(e >> 32);
             if (depth < kPrefixDepth) {
                 // leaf / void / fault above depth 4 (rare): its box is the one
                 // after `depth` splits
-                cur = dom;
-                for (int32_t l = 0; l < depth; ++l) split_box(cur, (cell >> (3 * (kPrefixDepth - 1 - l))) & 7u);
+                if (kPlanes && planes) {
+                    const uint32_t sh = static_cast<uint32_t>(kPrefixDepth - depth);
+                    const uint32_t w = 1u << sh;
+                    const uint32_t kx = (jx >> sh) << sh, ky = (jy >> sh) << sh, kz = (jz >> sh) << sh;
+                    cur = Box{pl[kx], pl[kPlaneStride + ky], pl[2 * kPlaneStride + kz],
+                              pl[kx + w], pl[kPlaneStride + ky + w], pl[2 * kPlaneStride + kz + w]};
+                } else {
+                    cur = dom;
+                    for (int32_t l = 0; l < depth; ++l) {
+                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
+                    }
+                }
             }
             const bool internal = slot < kSlotFault;  // an internal node at depth 4
             pre.x0 = internal ? cur.x0 : pre.x0;      // kernel.cu:154-163
@@ -448,7 +534,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
 // to exactly that, so no wave waits for a slot and the sweep has no second,
 // partly empty round.
 // (per LDS size of the launch; guarded by g_queue_mu).
-std::map<size_t, int> g_grid_blocks;
+std::map<std::pair<bool, size_t>, int> g_grid_blocks;
 
 // Work-queue counters, one pair per (device, stream), allocated once per device
 // at its first launch (a 2 KiB device buffer, zeroed then). Launches on one
@@ -490,11 +576,15 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.n_units = (P.n_rays + kUnitRays - 1u) / kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
-    const size_t lds = static_cast<size_t>(P.n_scenes) * sizeof(SceneLds);
+    const bool use_planes = P.n_scenes <= kPlaneScenes;
+    const size_t lds = static_cast<size_t>(P.n_scenes) *
+                       (sizeof(SceneLds) + (use_planes ? 3 * kPlaneStride * sizeof(float) : 0));
+    const auto kernel = use_planes ? trace_relaid_kernel<true> : trace_relaid_kernel<false>;
+    const auto key = std::make_pair(use_planes, lds);
     int grid_blocks = 0;
     {
         std::lock_guard<std::mutex> lock(g_queue_mu);
-        auto it = g_grid_blocks.find(lds);
+        auto it = g_grid_blocks.find(key);
         if (it != g_grid_blocks.end()) grid_blocks = it->second;
     }
     if (grid_blocks == 0) {
@@ -502,17 +592,16 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, trace_relaid_kernel, kThreads, lds) != hipSuccess ||
-            per_cu <= 0)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
             per_cu = 4;
         grid_blocks = cus * per_cu;
         std::lock_guard<std::mutex> lock(g_queue_mu);
-        g_grid_blocks[lds] = grid_blocks;
+        g_grid_blocks[key] = grid_blocks;
     }
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
     if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(trace_relaid_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;

@@ -198,8 +198,10 @@ def _walk(rec, root, cell):
     if root >> 31:
         return root, 0
     r = root
+    ix, iy, iz = cell & 15, (cell >> 4) & 15, cell >> 8
     for lvl in range(4):
-        oct_ = (cell >> (3 * (3 - lvl))) & 7
+        b = 3 - lvl
+        oct_ = ((ix >> b) & 1) | ((iy >> b) & 1) << 1 | ((iz >> b) & 1) << 2
         slot = int(rec[r][oct_]) if r < rec.shape[0] else 0x7FFFFFFE
         if slot >= 0x7FFFFFFE or lvl == 3:
             return slot, lvl + 1

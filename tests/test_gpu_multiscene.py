@@ -259,3 +259,30 @@ def test_relaid_descent_limit_chains(gpu, corpus):
         env_scene = np.array([0, len(picks) - 1], np.int32)
         ref = _oracle_multi([s[0] for s in scenes], [[0, 0, 0, 1, 1, 1]] * len(picks), env_scene, o, d, 12, 4.0)
         _compare(_run(res, env_scene, o, d, 12, 4.0), ref, 4.0, f"chains/{picks}")
+
+
+def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
+    """70 resident scenes (more than the launch keeps split planes for in LDS),
+    and domains too narrow for their magnitude (float split planes collapse),
+    both located by in-register splits instead of the plane lookup."""
+    from navi_amd.multiscene import ResidentScenes
+
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(70)]
+    res = ResidentScenes(many)
+    env_scene, o, d = _rays(corpus, 24, 16, 16, seed=31)
+    env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 70
+    ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 128, 30.0)
+    _compare(_run(res, env_scene, o, d, 128, 30.0, elevation_bins=16), ref, 30.0, "many")
+
+    words = corpus[0].words
+    narrow = [[1000.0, -2.0, 5.0, 1000.00048828125, 2.0, 5.0000019073486328],
+              [-1.0, -1.0, -1.0, 1.0, 1.0, 1.0]]
+    res = ResidentScenes([(words, b[:3], b[3:]) for b in narrow])
+    rng = np.random.default_rng(8)
+    env_scene = np.array([0, 1, 0], np.int32)
+    b = np.array(narrow, np.float64)[env_scene]
+    o = rng.uniform(b[:, None, :3], b[:, None, 3:], (3, 500, 3)).astype(np.float32)
+    d = rng.normal(size=(3, 500, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    ref = _oracle_multi([words] * 2, narrow, env_scene, o, d, 64, 5.0)
+    _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, "narrow")
