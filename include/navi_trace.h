@@ -80,7 +80,9 @@ int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, in
  * Device layout (no reference counterpart; it replaces how the reference reads
  * its words, kernel.cu:35-41,137-198). Converts a DAG in the reference word
  * layout (host memory) into 32-byte records of eight u32 octant slots in
- * breadth-first order: 0x7fffffff void, 0x7ffffffe out-of-range child, bit 31
+ * breadth-first order: 0x7fffffff void, 0x7ffffffe out-of-range child-table
+ * word, 0x7ffffffd out-of-range child index (a fault only where the child is
+ * examined, above the 32-level descent limit), bit 31
  * set = leaf inlined (bits 30..16 semantic, 15..0 fp16 distance), else a
  * record index. With out_records NULL only counts; otherwise writes up to
  * cap_records records. *root_slot is the root's slot value (0 = record 0, or
@@ -93,7 +95,7 @@ int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records
 
 /* One resident scene in the device layout (device memory, 48 bytes). Several
  * scenes share one record pool: scene records are concatenated and every child
- * record slot (a slot value below 0x7ffffffe) is rebased to an absolute pool
+ * record slot (a slot value below 0x7ffffffd) is rebased to an absolute pool
  * index by adding the scene's rec_offset; root_slot is rec_offset for an
  * internal root, or the inlined leaf of a one-leaf DAG. */
 typedef struct navi_relaid_scene {
@@ -150,6 +152,67 @@ int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_re
                       const float* dirs, float* out_distances, int32_t* out_semantics,
                       int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                       void* stream);
+
+/*
+ * navi_trace_relaid with the rays generated in the kernel from per-env poses
+ * (projects/environment/src/navi_environment/backends/sdfdag_backend.py:
+ * 1300-1312 computes them with tensor ops and hands 24 bytes per ray to the
+ * tracer): ray r of env e starts at env_pos[e] (3 floats) along
+ * (x c + z s, y, (-x) s + z c), (x, y, z) = local_dirs[r] (rays_per_env x 3
+ * floats, e.g. the az*El + el table of build_spherical_ray_directions,
+ * :205-221) and (c, s) = env_rot[e] (cos and sin of the env's yaw). Each
+ * product and sum is rounded on its own, as in the reference's eager tensor
+ * code, so the rays are bit-identical to ones built that way from the same
+ * cos / sin values. Everything else as navi_trace_relaid.
+ */
+int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                            int32_t n_scenes, const uint64_t* root_tables, const int32_t* env_scene,
+                            const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
+                            int32_t elevation_bins, const float* local_dirs, const float* env_pos,
+                            const float* env_rot, float* out_distances, int32_t* out_semantics,
+                            int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
+                            void* stream);
+
+/*
+ * Point-SDF queries (no reference kernel; the query of
+ * projects/torch-sdf/cpp_src/kernel.cu:88-200 from the root, without caches)
+ * over the device layout. Point i (3 floats) is looked up in scene
+ * point_scene[i] (NULL: scene 0). Outputs per point: distance, semantic and,
+ * if out_kind is non-NULL, the kind: 0 outside the scene box (1000, 0);
+ * 1 leaf (its fp16 distance and semantic); 2 void cell (side along x times
+ * 1.7321: the compiler prunes an octant only when every sample in it clears
+ * its half-diagonal, projects/voxel-dag/src/compiler.cpp:626,639-643, so this
+ * is a clearance lower bound; semantic 0); 3 the 32-level limit (NaN, 0);
+ * 4 out-of-range data or an unknown scene id (NaN, 0).
+ */
+int navi_point_query(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                     int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene,
+                     const float* points, int64_t n_points, float* out_distances, int32_t* out_semantics,
+                     int32_t* out_kind, void* stream);
+
+/*
+ * Observation post-pass in one launch (replaces the tensor code of
+ * projects/environment/src/navi_environment/backends/sdfdag_backend.py:
+ * 366-473 and the collision test of :1340), optionally fused with point
+ * queries (as navi_point_query; n_points 0 for none). distances is
+ * n_envs x (azimuth_bins * elevation_bins) floats, flat index az * El + el.
+ * Per env: clamped c = clamp(d, 0, max_distance) (NaN stays NaN);
+ * out_depth_f16 (optional, IEEE binary16, n_envs x El x Az: transposed)
+ * = clamp(log1p(c) / log1p(max_distance), 0, 1); out_stats (optional,
+ * n_envs x 5 floats) = min c (NaN if any is NaN), starvation ratio
+ * (c >= max_distance - 1e-3), proximity ratio (finite and
+ * c <= proximity_threshold; 0 if the threshold is <= 0), structure-band ratio
+ * (finite and band_min <= c <= band_max; 0 unless band_max > band_min) and
+ * forward structure ratio (the same over the first and last max(1, Az / 6)
+ * azimuth bins); out_collision (optional, n_envs int32) = min c <
+ * collision_clearance.
+ */
+int navi_observe(const float* distances, int64_t n_envs, int32_t azimuth_bins, int32_t elevation_bins,
+                 float max_distance, float structure_band_min, float structure_band_max, float proximity_threshold,
+                 float collision_clearance, void* out_depth_f16, float* out_stats, int32_t* out_collision,
+                 const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes, int32_t n_scenes,
+                 const uint64_t* root_tables, const int32_t* point_scene, const float* points, int64_t n_points,
+                 float* point_distances, int32_t* point_semantics, int32_t* point_kind, void* stream);
 
 /* Message of the last failure on the calling thread ("" if none). The
  * reference surfaces failures as c10::Error via TORCH_CHECK (bindings.cpp:57-89). */

@@ -61,6 +61,21 @@ _lib.navi_trace_relaid.argtypes = [
     _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 
+_lib.navi_trace_relaid_poses.restype = ctypes.c_int
+_lib.navi_trace_relaid_poses.argtypes = [
+    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp,
+    _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
+]
+_lib.navi_point_query.restype = ctypes.c_int
+_lib.navi_point_query.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, _vp, _vp,
+                                  _vp, _vp]
+_lib.navi_observe.restype = ctypes.c_int
+_lib.navi_observe.argtypes = [
+    _vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+    ctypes.c_float, ctypes.c_float, _vp, _vp, _vp, _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp,
+    ctypes.c_int64, _vp, _vp, _vp, _vp,
+]
+
 # Layout of navi_relaid_scene (include/navi_trace.h), 48 bytes.
 RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot", "<u4"),
                       ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,)), ("max_depth", "<u4"),

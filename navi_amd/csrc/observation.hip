@@ -1,0 +1,292 @@
+// observation.hip — what the caller does with a trace, on the device: the
+// observation post-pass (clamp, log-normalise, fp16 pack, per-env ratios and
+// clearance, projects/environment/src/navi_environment/backends/
+// sdfdag_backend.py:366-473 and :1340 of the seismael/navi checkout) and
+// point-SDF queries over the device record layout, fused into one launch.
+//
+// Post-pass: one workgroup per env. The env's Az * El distances (flat index
+// az * El + el) are read once, coalesced; every thread keeps counts and the
+// minimum in registers, the workgroup reduces them through LDS, and thread 0
+// writes the env's statistics. The fp16 depth is written transposed,
+// (env, 1, El, Az), the layout the policy consumes.
+//
+// Point queries: one lane per point, a fresh descent with no caches (the
+// query of kernel.cu:88-200 from the root): the root table gives the first
+// four levels, record reads the rest.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "navi_trace.h"
+#include "trace_common.hpp"
+
+namespace navi {
+
+int set_error(int code, const char* fmt, ...);
+
+namespace {
+
+constexpr uint32_t kSlotVoid = 0x7fffffffu;
+constexpr uint32_t kSlotFault = 0x7ffffffeu;
+constexpr uint32_t kSlotBadChild = 0x7ffffffdu;
+constexpr int kThreads = 256;
+constexpr float kVoidClearance = 1.7321f;  // compiler.cpp:626,639-643: pruned octants clear half-diagonal
+
+enum : int32_t { kKindOutside = 0, kKindLeaf = 1, kKindVoid = 2, kKindDepth = 3, kKindFault = 4 };
+
+struct PostParams {
+    const float* __restrict__ dist;  // [n_envs][az * el]
+    int32_t n_envs, az, el;
+    float max_distance, band_min, band_max, proximity, clearance;
+    // The reference compares float32 tensors with Python floats and divides
+    // by one: the host rounds max_distance - 1e-3 and log1p(max_distance),
+    // evaluated in double, to float, as torch does with such scalars.
+    float saturation, log_denom;
+    _Float16* __restrict__ depth16;  // [n_envs][el][az] or null
+    float* __restrict__ stats;       // [n_envs][5] or null
+    int32_t* __restrict__ collision;  // [n_envs] or null
+    // point queries
+    const uint32_t* __restrict__ records;
+    uint32_t n_records;
+    const navi_relaid_scene* __restrict__ scenes;
+    int32_t n_scenes;
+    const uint64_t* __restrict__ root_table;
+    const int32_t* __restrict__ point_scene;  // [n_points] or null (scene 0)
+    const float* __restrict__ points;         // [n_points][3]
+    int32_t n_points;
+    float* __restrict__ point_d;
+    int32_t* __restrict__ point_s;
+    int32_t* __restrict__ point_kind;  // or null
+    int32_t env_blocks;                // workgroups doing the post-pass; the rest do points
+};
+
+// kernel.cu:88-200 from the root at one point, no caches. Outside the domain:
+// (1000, 0); leaf: its distance and semantic; void: the void cell's clearance
+// bound, side * 1.7321; 32 levels without a result: NaN; out-of-range data: NaN.
+__device__ void point_query(const PostParams& P, int32_t i) {
+    const int32_t sc = P.point_scene ? P.point_scene[i] : 0;
+    float d = __builtin_nanf("");
+    int32_t s = 0, kind = kKindFault;
+    if (sc >= 0 && sc < P.n_scenes) {
+        const navi_relaid_scene S = P.scenes[sc];
+        const float px = P.points[3 * i + 0], py = P.points[3 * i + 1], pz = P.points[3 * i + 2];
+        const Box dom{S.bbox_min[0], S.bbox_min[1], S.bbox_min[2], S.bbox_max[0], S.bbox_max[1], S.bbox_max[2]};
+        if (!in_box(px, py, pz, dom)) {
+            d = kOutsideDomain;
+            kind = kKindOutside;
+        } else {
+            Box cur = dom;
+            uint32_t slot = S.root_slot;
+            int32_t depth = 0;
+            if (!(slot & 0x80000000u)) {
+                uint32_t jx = 0, jy = 0, jz = 0;
+                for (int l = 0; l < kPrefixDepth; ++l) {
+                    const uint32_t oct = descend_octant(px, py, pz, cur);
+                    jx = 2u * jx + (oct & 1u);
+                    jy = 2u * jy + ((oct >> 1) & 1u);
+                    jz = 2u * jz + (oct >> 2);
+                }
+                const uint64_t e = P.root_table[((((uint32_t)sc << 4 | jz) << 4 | jy) << 4) | jx];
+                slot = static_cast<uint32_t>(e);
+                depth = static_cast<int32_t>(e >> 32);
+                if (depth < kPrefixDepth) {
+                    cur = dom;
+                    for (int32_t l = 0; l < depth; ++l) {
+                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
+                    }
+                }
+                while (slot < kSlotBadChild && depth < kMaxDepth) {
+                    const uint32_t oct = descend_octant(px, py, pz, cur);
+                    slot = P.records[8u * min(slot, P.n_records - 1u) + oct];
+                    ++depth;
+                }
+            }
+            if (slot & 0x80000000u) {
+                if (depth < kMaxDepth) {
+                    d = half_to_float(slot & 0xffffu);
+                    s = static_cast<int32_t>((slot >> 16) & 0x7fffu);
+                    kind = kKindLeaf;
+                } else {
+                    kind = kKindDepth;
+                }
+            } else if (slot == kSlotVoid) {
+                d = (cur.x1 - cur.x0) * kVoidClearance;
+                kind = kKindVoid;
+            } else if (slot == kSlotFault || (slot == kSlotBadChild && depth < kMaxDepth)) {
+                kind = kKindFault;
+            } else {
+                kind = kKindDepth;
+            }
+        }
+    }
+    P.point_d[i] = d;
+    P.point_s[i] = s;
+    if (P.point_kind) P.point_kind[i] = kind;
+}
+
+template <typename T>
+__device__ T block_sum(T v, T* lds) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[w] = v;
+    __syncthreads();
+    T r = 0;
+    for (int k = 0; k < kThreads / 64; ++k) r += lds[k];
+    return r;
+}
+
+// torch.amin semantics: NaN if any input is NaN.
+__device__ float nan_min(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
+
+__device__ float block_min(float v, float* lds) {
+    for (int off = 32; off > 0; off >>= 1) v = nan_min(v, __shfl_xor(v, off));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) lds[w] = v;
+    __syncthreads();
+    float r = lds[0];
+    for (int k = 1; k < kThreads / 64; ++k) r = nan_min(r, lds[k]);
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
+    if (static_cast<int32_t>(blockIdx.x) >= P.env_blocks) {
+        const int32_t i = (static_cast<int32_t>(blockIdx.x) - P.env_blocks) * kThreads + threadIdx.x;
+        if (i < P.n_points) point_query(P, i);
+        return;
+    }
+    __shared__ uint32_t lds_u[kThreads / 64];
+    __shared__ float lds_f[kThreads / 64];
+    const int32_t e = blockIdx.x;
+    const int32_t n = P.az * P.el;
+    const float* dist = P.dist + static_cast<int64_t>(e) * n;
+    // sdfdag_backend.py:390: the first and last Az/6 azimuth bins (at least one)
+    const int32_t fwd = max(1, P.az / 6);
+    const bool band = P.band_max > P.band_min;
+    uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0;
+    float mn = INFINITY;
+    for (int32_t k = threadIdx.x; k < n; k += kThreads) {
+        const float m = dist[k];
+        const bool valid = isfinite(m);
+        // torch.clamp(min=0, max=max_distance): NaN stays NaN
+        const float c = (m != m) ? m : fminf(fmaxf(m, 0.0f), P.max_distance);
+        mn = nan_min(mn, c);
+        n_sat += (c >= P.saturation) ? 1u : 0u;
+        n_prox += (valid && c <= P.proximity) ? 1u : 0u;
+        const bool in_band = band && valid && c >= P.band_min && c <= P.band_max;
+        n_band += in_band ? 1u : 0u;
+        const int32_t a = k / P.el;
+        // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
+        n_fwd += in_band ? static_cast<uint32_t>((a < fwd ? 1 : 0) + (a >= P.az - fwd ? 1 : 0)) : 0u;
+        if (P.depth16) {
+            const float q = c != c ? c : fminf(fmaxf(log1pf(c) / P.log_denom, 0.0f), 1.0f);
+            P.depth16[static_cast<int64_t>(e) * n + static_cast<int64_t>(k % P.el) * P.az + a] =
+                static_cast<_Float16>(q);
+        }
+    }
+    n_sat = block_sum(n_sat, lds_u);
+    n_prox = block_sum(n_prox, lds_u);
+    n_band = block_sum(n_band, lds_u);
+    n_fwd = block_sum(n_fwd, lds_u);
+    mn = block_min(mn, lds_f);
+    if (threadIdx.x == 0) {
+        const float fn = static_cast<float>(n);
+        if (P.stats) {
+            float* st = P.stats + 5 * static_cast<int64_t>(e);
+            st[0] = mn;
+            st[1] = static_cast<float>(n_sat) / fn;
+            st[2] = P.proximity > 0.0f ? static_cast<float>(n_prox) / fn : 0.0f;
+            st[3] = band ? static_cast<float>(n_band) / fn : 0.0f;
+            st[4] = band ? static_cast<float>(n_fwd) / static_cast<float>(2 * fwd * P.el) : 0.0f;
+        }
+        if (P.collision) P.collision[e] = mn < P.clearance ? 1 : 0;  // sdfdag_backend.py:1340
+    }
+}
+
+int launch(const PostParams& P, hipStream_t stream) {
+    const int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
+    const int64_t blocks = static_cast<int64_t>(P.env_blocks) + point_blocks;
+    if (blocks == 0) return NAVI_OK;
+    hipLaunchKernelGGL(observation_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, P);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    return NAVI_OK;
+}
+
+int points_setup(PostParams& P, const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                 int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene, const float* points,
+                 int64_t n_points, float* out_d, int32_t* out_s, int32_t* out_kind) {
+    if (n_points < 0 || n_points > (1LL << 30)) return set_error(NAVI_E_ARG, "n_points must be in [0, 2^30]");
+    if (n_points == 0) return NAVI_OK;
+    if (!points || !out_d || !out_s) return set_error(NAVI_E_ARG, "points and point outputs must be non-null");
+    if (n_scenes <= 0 || !scenes || !records || !root_tables)
+        return set_error(NAVI_E_ARG, "scene table, records and root_tables must be non-empty");
+    if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
+    P.records = records;
+    P.n_records = static_cast<uint32_t>(n_records);
+    P.scenes = scenes;
+    P.n_scenes = n_scenes;
+    P.root_table = root_tables;
+    P.point_scene = point_scene;
+    P.points = points;
+    P.n_points = static_cast<int32_t>(n_points);
+    P.point_d = out_d;
+    P.point_s = out_s;
+    P.point_kind = out_kind;
+    return NAVI_OK;
+}
+
+}  // namespace
+}  // namespace navi
+
+extern "C" int navi_point_query(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                                int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene,
+                                const float* points, int64_t n_points, float* out_distances,
+                                int32_t* out_semantics, int32_t* out_kind, void* stream) {
+    using namespace navi;
+    PostParams P{};
+    const int code = points_setup(P, records, n_records, scenes, n_scenes, root_tables, point_scene, points, n_points,
+                                  out_distances, out_semantics, out_kind);
+    if (code != NAVI_OK || n_points == 0) return code;
+    return launch(P, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int navi_observe(const float* distances, int64_t n_envs, int32_t azimuth_bins, int32_t elevation_bins,
+                            float max_distance, float structure_band_min, float structure_band_max,
+                            float proximity_threshold, float collision_clearance, void* out_depth_f16,
+                            float* out_stats, int32_t* out_collision, const uint32_t* records,
+                            uint64_t n_records, const navi_relaid_scene* scenes, int32_t n_scenes,
+                            const uint64_t* root_tables, const int32_t* point_scene, const float* points,
+                            int64_t n_points, float* point_distances, int32_t* point_semantics,
+                            int32_t* point_kind, void* stream) {
+    using namespace navi;
+    if (n_envs < 0 || n_envs > 0x7fffffffLL) return set_error(NAVI_E_ARG, "n_envs must be in [0, 2^31)");
+    if (azimuth_bins <= 0 || elevation_bins <= 0 ||
+        static_cast<int64_t>(azimuth_bins) * elevation_bins > 0x7fffffffLL)
+        return set_error(NAVI_E_ARG, "azimuth_bins and elevation_bins must be positive");
+    if (!std::isfinite(max_distance) || !(max_distance > 0.0f))
+        return set_error(NAVI_E_ARG, "max_distance must be a finite positive float");
+    if (n_envs > 0 && !distances) return set_error(NAVI_E_ARG, "distances must be non-null");
+    PostParams P{};
+    P.dist = distances;
+    P.n_envs = static_cast<int32_t>(n_envs);
+    P.az = azimuth_bins;
+    P.el = elevation_bins;
+    P.max_distance = max_distance;
+    P.saturation = static_cast<float>(static_cast<double>(max_distance) - 1e-3);
+    P.log_denom = static_cast<float>(std::log1p(static_cast<double>(max_distance)));
+    P.band_min = structure_band_min;
+    P.band_max = structure_band_max;
+    P.proximity = proximity_threshold;
+    P.clearance = collision_clearance;
+    P.depth16 = static_cast<_Float16*>(out_depth_f16);
+    P.stats = out_stats;
+    P.collision = out_collision;
+    P.env_blocks = static_cast<int32_t>(n_envs);
+    const int code = points_setup(P, records, n_records, scenes, n_scenes, root_tables, point_scene, points, n_points,
+                                  point_distances, point_semantics, point_kind);
+    if (code != NAVI_OK) return code;
+    return launch(P, static_cast<hipStream_t>(stream));
+}

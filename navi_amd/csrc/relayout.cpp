@@ -12,7 +12,11 @@
 // breadth-first order from the root (so the top levels are a contiguous
 // prefix), each holding eight u32 slots indexed by octant:
 //   0x7fffffff             void octant (mask bit clear)
-//   0x7ffffffe             the reference would read past the array here
+//   0x7ffffffe             the child-table word lies past the array: the
+//                          reference reads out of range at this level
+//   0x7ffffffd             the child index lies past the array: the reference
+//                          reads out of range when it examines the child
+//                          (only below the 32-level limit of kernel.cu:136)
 //   bit 31 set             leaf inlined: bits 30..16 semantic, 15..0 fp16 distance
 //   otherwise              index of the child's record
 // Descending one level is one 4-byte load at record*8 + octant, and a leaf
@@ -20,7 +24,7 @@
 // caches key on boxes, which depend only on the tree shape.
 //
 // Not representable (NAVI_E_LAYOUT; use the reference-layout kernel): a leaf
-// reachable from the root with semantic > 0x7fff, or more than 0x7ffffffd
+// reachable from the root with semantic > 0x7fff, or more than 0x7ffffffc
 // internal nodes.
 #include <stdint.h>
 
@@ -37,13 +41,14 @@ namespace {
 
 constexpr uint32_t kSlotVoid = 0x7fffffffu;
 constexpr uint32_t kSlotFault = 0x7ffffffeu;
+constexpr uint32_t kSlotBadChild = 0x7ffffffdu;  // lowest terminal slot value
 constexpr uint32_t kUnassigned = 0xffffffffu;
 
 // Slot value for a child word index, assigning record ids on first sight.
 inline bool child_slot(const uint64_t* w, uint64_t n, uint32_t idx, std::vector<uint32_t>& rec_of,
                        std::vector<uint32_t>& queue, uint32_t& out) {
     if (static_cast<uint64_t>(idx) >= n) {
-        out = kSlotFault;
+        out = kSlotBadChild;
         return true;
     }
     const uint64_t node = w[idx];
@@ -54,7 +59,7 @@ inline bool child_slot(const uint64_t* w, uint64_t n, uint32_t idx, std::vector<
         return true;
     }
     if (rec_of[idx] == kUnassigned) {
-        if (queue.size() >= kSlotFault) return false;
+        if (queue.size() >= kSlotBadChild) return false;
         rec_of[idx] = static_cast<uint32_t>(queue.size());
         queue.push_back(idx);
     }
@@ -151,7 +156,7 @@ extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records
                 const uint32_t oct = ((c >> b) & 1u) | (((c >> (4u + b)) & 1u) << 1) | (((c >> (8u + b)) & 1u) << 2);
                 slot = static_cast<uint64_t>(r) < n_records ? records[8ull * r + oct] : kSlotFault;
                 d = l + 1u;
-                if (slot >= kSlotFault || d == 4u) break;
+                if (slot >= kSlotBadChild || d == 4u) break;
                 r = slot;
             }
         }
@@ -170,7 +175,7 @@ extern "C" int navi_record_depth(const uint32_t* records, uint64_t n_records, ui
                                  uint32_t* max_depth) {
     using navi::set_error;
     if (!max_depth || (!records && n_records)) return set_error(NAVI_E_ARG, "null argument");
-    if (root_slot >= kSlotFault) {  // one-leaf DAG (or a void / fault root slot)
+    if (root_slot >= kSlotBadChild) {  // one-leaf DAG (or a void / fault root slot)
         *max_depth = 0;
         return NAVI_OK;
     }
@@ -200,7 +205,7 @@ extern "C" int navi_record_depth(const uint32_t* records, uint64_t n_records, ui
             continue;
         }
         const uint32_t slot = records[8ull * f.rec + f.next++];
-        if (slot >= kSlotFault) continue;  // leaf, void or fault slot
+        if (slot >= kSlotBadChild) continue;  // leaf, void or fault slot
         if (slot >= n_records) {
             *max_depth = 0xffffffffu;
             return NAVI_OK;

@@ -41,7 +41,8 @@ namespace navi {
 int set_error(int code, const char* fmt, ...);
 
 constexpr uint32_t kSlotVoid = 0x7fffffffu;
-constexpr uint32_t kSlotFault = 0x7ffffffeu;
+constexpr uint32_t kSlotFault = 0x7ffffffeu;     // child-table word out of range
+constexpr uint32_t kSlotBadChild = 0x7ffffffdu;  // child index out of range; lowest terminal value
 
 // Division by a runtime-invariant divisor d >= 1 (Granlund-Montgomery):
 // n / d = (t + ((n - t) >> 1)) >> (l - 1), t = mulhi(n, m), for all 32-bit n.
@@ -80,8 +81,13 @@ struct RelaidParams {
     FastDiv div_rays;      // by rays_per_env
     uint32_t tile_el;      // elevation bins when 8x8 tiling applies, else 0
     FastDiv div_tiles_el;  // by tile_el / 8
-    const float* __restrict__ origins;
+    const float* __restrict__ origins;  // [n_rays][3], or null with local_dirs
     const float* __restrict__ dirs;
+    // Ray generation from poses (when local_dirs is non-null): ray r of env e
+    // starts at env_pos[e] along R_y(yaw_e) local_dirs[r], env_rot[e] = (cos, sin).
+    const float* __restrict__ local_dirs;  // [rays_per_env][3]
+    const float* __restrict__ env_pos;     // [n_envs][3]
+    const float* __restrict__ env_rot;     // [n_envs][2]
     float* __restrict__ out_d;
     int32_t* __restrict__ out_s;
     int32_t* __restrict__ out_steps;
@@ -271,12 +277,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 int32_t env;
                 ray = ray_of(P, q, env);
                 const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
-                ox = P.origins[3 * ray + 0];
-                oy = P.origins[3 * ray + 1];
-                oz = P.origins[3 * ray + 2];
-                dx = P.dirs[3 * ray + 0];
-                dy = P.dirs[3 * ray + 1];
-                dz = P.dirs[3 * ray + 2];
+                if (P.local_dirs != nullptr) {
+                    // sdfdag_backend.py:1300-1312: origin = the env's position;
+                    // x' = x c + z s, y' = y, z' = (-x) s + z c, each product
+                    // and sum rounded on its own as in the eager tensor code
+                    const uint32_t r = ray - static_cast<uint32_t>(env) * P.rays_per_env;
+                    const float c = P.env_rot[2 * env], s = P.env_rot[2 * env + 1];
+                    const float lx = P.local_dirs[3 * r + 0];
+                    const float ly = P.local_dirs[3 * r + 1];
+                    const float lz = P.local_dirs[3 * r + 2];
+                    ox = P.env_pos[3 * env + 0];
+                    oy = P.env_pos[3 * env + 1];
+                    oz = P.env_pos[3 * env + 2];
+                    dx = lx * c + lz * s;
+                    dy = ly;
+                    dz = (-lx) * s + lz * c;
+                } else {
+                    ox = P.origins[3 * ray + 0];
+                    oy = P.origins[3 * ray + 1];
+                    oz = P.origins[3 * ray + 2];
+                    dx = P.dirs[3 * ray + 0];
+                    dy = P.dirs[3 * ray + 1];
+                    dz = P.dirs[3 * ray + 2];
+                }
                 rx = 1.0f / dx;  // correctly rounded (IEEE division)
                 ry = 1.0f / dy;
                 rz = 1.0f / dz;
@@ -390,7 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     }
                 }
             }
-            const bool internal = slot < kSlotFault;  // an internal node at depth 4
+            const bool internal = slot < kSlotBadChild;  // an internal node at depth 4
             pre.x0 = internal ? cur.x0 : pre.x0;      // kernel.cu:154-163
             pre.y0 = internal ? cur.y0 : pre.y0;
             pre.z0 = internal ? cur.z0 : pre.z0;
@@ -412,14 +435,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             while (descending) {
                 slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
                 cur_rec = slot;  // read again only while internal
-                descending = slot < kSlotFault;
+                descending = slot < kSlotBadChild;
             }
         } else {
             while (descending) {
                 slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
                 depth += 1;
                 cur_rec = slot;
-                descending = slot < kSlotFault && depth < kMaxDepth;
+                descending = slot < kSlotBadChild && depth < kMaxDepth;
             }
         }
 
@@ -427,7 +450,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         const bool leaf_child = (slot & 0x80000000u) != 0u && (shallow || depth < kMaxDepth);  // examined at depth < 32
         const bool is_void = hit_vd || (!cached && slot == kSlotVoid);
         const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
-        const bool is_fault = !cached && slot == kSlotFault;
+        // a bad child index faults only where the reference examines the
+        // child, above the 32-level limit; at depth 32 the result is stale
+        const bool is_fault = !cached && (slot == kSlotFault ||
+                                          (slot == kSlotBadChild && (shallow || depth < kMaxDepth)));
         const bool new_void = did_descend && is_void;
         const bool new_leaf = !cached && is_leaf;  // from a descent
         vd.x0 = new_void ? cur.x0 : vd.x0;
@@ -609,14 +635,14 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
 
 }  // namespace navi
 
-extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                                 int32_t n_scenes, const uint64_t* root_tables,
-                                 const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
-                                 int64_t rays_per_env, int32_t elevation_bins, const float* origins,
-                                 const float* dirs, float* out_distances, int32_t* out_semantics,
-                                 int32_t max_steps, float max_distance, float hit_epsilon,
-                                 int32_t* out_steps, void* stream) {
-    using namespace navi;
+namespace navi {
+
+// Arguments shared by the two relaid entry points.
+int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                 int32_t n_scenes, const uint64_t* root_tables, const int32_t* env_scene,
+                 const int32_t* env_order, int64_t n_envs, int64_t rays_per_env, int32_t elevation_bins,
+                 float* out_distances, int32_t* out_semantics, int32_t max_steps, float max_distance,
+                 float hit_epsilon, int32_t* out_steps) {
     if (max_steps <= 0) return set_error(NAVI_E_ARG, "max_steps must be a positive integer");
     if (!std::isfinite(max_distance) || !(max_distance > 0.0f))
         return set_error(NAVI_E_ARG, "max_distance must be a finite positive float");
@@ -628,13 +654,12 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
     // 32-bit slot addressing: record * 8 + octant must fit in uint32
     if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
     const int64_t n_rays = n_envs * rays_per_env;
-    if (n_rays == 0) return NAVI_OK;
     // 32-bit work indexing: every ray index times 3 must fit in uint32
     if (n_rays > 0x3fffffffLL || rays_per_env > 0x3fffffffLL)
         return set_error(NAVI_E_ARG, "navi_trace_relaid handles at most 2^30 rays per launch");
-    if (!origins || !dirs || !out_distances || !out_semantics)
-        return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
-    RelaidParams P{};
+    if (n_rays > 0 && (!out_distances || !out_semantics))
+        return set_error(NAVI_E_ARG, "output pointers must be non-null");
+    P = RelaidParams{};
     P.records = records;
     P.n_records = static_cast<uint32_t>(n_records);
     P.scenes = scenes;
@@ -649,13 +674,54 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
                     ? static_cast<uint32_t>(elevation_bins)
                     : 0u;
     P.div_tiles_el = make_fastdiv(P.tile_el ? P.tile_el / 8u : 1u);
-    P.origins = origins;
-    P.dirs = dirs;
     P.out_d = out_distances;
     P.out_s = out_semantics;
     P.out_steps = out_steps;
     P.max_steps = max_steps;
     P.max_distance = max_distance;
     P.hit_eps = hit_epsilon;
+    return NAVI_OK;
+}
+
+}  // namespace navi
+
+extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                                 int32_t n_scenes, const uint64_t* root_tables,
+                                 const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
+                                 int64_t rays_per_env, int32_t elevation_bins, const float* origins,
+                                 const float* dirs, float* out_distances, int32_t* out_semantics,
+                                 int32_t max_steps, float max_distance, float hit_epsilon,
+                                 int32_t* out_steps, void* stream) {
+    using namespace navi;
+    RelaidParams P;
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, env_scene, env_order, n_envs,
+                                  rays_per_env, elevation_bins, out_distances, out_semantics, max_steps,
+                                  max_distance, hit_epsilon, out_steps);
+    if (code != NAVI_OK || P.n_rays == 0) return code;
+    if (!origins || !dirs) return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
+    P.origins = origins;
+    P.dirs = dirs;
+    return launch_relaid(P, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records,
+                                       const navi_relaid_scene* scenes, int32_t n_scenes,
+                                       const uint64_t* root_tables, const int32_t* env_scene,
+                                       const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
+                                       int32_t elevation_bins, const float* local_dirs, const float* env_pos,
+                                       const float* env_rot, float* out_distances, int32_t* out_semantics,
+                                       int32_t max_steps, float max_distance, float hit_epsilon,
+                                       int32_t* out_steps, void* stream) {
+    using namespace navi;
+    RelaidParams P;
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, env_scene, env_order, n_envs,
+                                  rays_per_env, elevation_bins, out_distances, out_semantics, max_steps,
+                                  max_distance, hit_epsilon, out_steps);
+    if (code != NAVI_OK || P.n_rays == 0) return code;
+    if (!local_dirs || !env_pos || !env_rot)
+        return set_error(NAVI_E_ARG, "local_dirs, env_pos and env_rot must be non-null");
+    P.local_dirs = local_dirs;
+    P.env_pos = env_pos;
+    P.env_rot = env_rot;
     return launch_relaid(P, static_cast<hipStream_t>(stream));
 }

@@ -71,7 +71,7 @@ class ResidentScenes:
             rtable[i]["n_records"] = rec.shape[0]
             # child record slots become absolute pool indices
             rec = rec.copy()
-            child = rec < 0x7FFFFFFE
+            child = rec < 0x7FFFFFFD
             rec[child] += np.uint32(roff)
             rtable[i]["root_slot"] = root if root & 0x80000000 else roff + root
             rtable[i]["bbox_min"] = table[i]["bbox_min"]
@@ -163,4 +163,106 @@ class ResidentScenes:
                 int(max_steps), float(max_distance), float(hit_epsilon),
                 out_steps.data_ptr() if out_steps is not None else None,
                 out_words.data_ptr() if out_words is not None else None, stream)
+        _native.check(code)
+
+    # ---- pose-driven tracing, point queries and the observation post-pass ----
+
+    def _require_relaid(self) -> None:
+        if not self.relaid_ok:
+            raise RuntimeError("these scenes do not fit the device record layout "
+                               "(leaf semantic above 0x7fff or more than 2^29 records)")
+
+    def _check(self, name: str, t: Any, dtype: Any, shape: tuple[int, ...], optional: bool = False) -> int | None:
+        if t is None:
+            if optional:
+                return None
+            raise RuntimeError(f"{name} is required")
+        if t.device != self.device or t.dtype != dtype or not t.is_contiguous() or tuple(t.shape) != shape:
+            raise RuntimeError(f"{name} must be a contiguous {dtype} tensor of shape {shape} on {self.device}")
+        return t.data_ptr()
+
+    def cast_rays_poses(self, env_scene: torch.Tensor, local_dirs: torch.Tensor, env_pos: torch.Tensor,
+                        env_rot: torch.Tensor, out_distances: torch.Tensor, out_semantics: torch.Tensor,
+                        max_steps: int, max_distance: float, *, hit_epsilon: float = 0.01,
+                        out_steps: Any | None = None, elevation_bins: int | None = None,
+                        sort_by_scene: bool = True) -> None:
+        """Trace with rays generated in the kernel: env ``e`` casts ``local_dirs`` ``[R, 3]``
+        rotated by its yaw (``env_rot[e] = (cos, sin)``) from ``env_pos[e]``, the ray layout
+        of ``sdfdag_backend.py:1300-1312``. Outputs ``[E, R]`` as ``cast_rays``."""
+        self._require_relaid()
+        e, r = int(env_pos.shape[0]), int(local_dirs.shape[0])
+        ptrs = [self._check("env_scene", env_scene, torch.int32, (e,)),
+                self._check("local_dirs", local_dirs, torch.float32, (r, 3)),
+                self._check("env_pos", env_pos, torch.float32, (e, 3)),
+                self._check("env_rot", env_rot, torch.float32, (e, 2)),
+                self._check("out_distances", out_distances, torch.float32, (e, r)),
+                self._check("out_semantics", out_semantics, torch.int32, (e, r)),
+                self._check("out_steps", out_steps, torch.int32, (e, r), optional=True)]
+        order = self.env_order(env_scene) if sort_by_scene else None
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            code = _native.lib().navi_trace_relaid_poses(
+                self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
+                self.root_tables.data_ptr(), ptrs[0], order.data_ptr() if order is not None else None, e, r,
+                int(elevation_bins or 0), ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], int(max_steps),
+                float(max_distance), float(hit_epsilon), ptrs[6], stream)
+        _native.check(code)
+
+    def point_query(self, points: torch.Tensor, out_distances: torch.Tensor, out_semantics: torch.Tensor, *,
+                    point_scene: torch.Tensor | None = None, out_kind: torch.Tensor | None = None) -> None:
+        """Point-SDF queries ``points [P, 3]`` (scene ``point_scene[i]``, default 0); see
+        ``navi_point_query`` in ``include/navi_trace.h`` for the result kinds."""
+        self._require_relaid()
+        p = int(points.shape[0])
+        ptrs = [self._check("points", points, torch.float32, (p, 3)),
+                self._check("out_distances", out_distances, torch.float32, (p,)),
+                self._check("out_semantics", out_semantics, torch.int32, (p,)),
+                self._check("point_scene", point_scene, torch.int32, (p,), optional=True),
+                self._check("out_kind", out_kind, torch.int32, (p,), optional=True)]
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            code = _native.lib().navi_point_query(
+                self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
+                self.root_tables.data_ptr(), ptrs[3], ptrs[0], p, ptrs[1], ptrs[2], ptrs[4], stream)
+        _native.check(code)
+
+    def observe(self, distances: torch.Tensor, azimuth_bins: int, elevation_bins: int, max_distance: float, *,
+                structure_band_min: float = 1.5, structure_band_max: float = 30.0,
+                proximity_threshold: float = 2.0, collision_clearance: float = 0.15,
+                out_depth_f16: torch.Tensor | None = None, out_stats: torch.Tensor | None = None,
+                out_collision: torch.Tensor | None = None, points: torch.Tensor | None = None,
+                point_scene: torch.Tensor | None = None, point_distances: torch.Tensor | None = None,
+                point_semantics: torch.Tensor | None = None, point_kind: torch.Tensor | None = None) -> None:
+        """The observation post-pass of ``sdfdag_backend.py:366-473,1340`` in one launch, with
+        optional point queries fused in. ``distances [E, Az*El]``; writes ``out_depth_f16
+        [E, 1, El, Az]`` (float16), ``out_stats [E, 5]`` (min distance, starvation, proximity,
+        structure-band and forward-structure ratios), ``out_collision [E]`` (int32). Defaults
+        are the reference's (``sdfdag_backend.py:38,48-51``)."""
+        e = int(distances.shape[0])
+        n = int(azimuth_bins) * int(elevation_bins)
+        d_ptr = self._check("distances", distances, torch.float32, (e, n))
+        outs = [self._check("out_depth_f16", out_depth_f16, torch.float16,
+                            (e, 1, int(elevation_bins), int(azimuth_bins)), optional=True),
+                self._check("out_stats", out_stats, torch.float32, (e, 5), optional=True),
+                self._check("out_collision", out_collision, torch.int32, (e,), optional=True)]
+        n_pts = 0
+        pp = [None] * 5
+        if points is not None:
+            self._require_relaid()
+            n_pts = int(points.shape[0])
+            pp = [self._check("points", points, torch.float32, (n_pts, 3)),
+                  self._check("point_scene", point_scene, torch.int32, (n_pts,), optional=True),
+                  self._check("point_distances", point_distances, torch.float32, (n_pts,)),
+                  self._check("point_semantics", point_semantics, torch.int32, (n_pts,)),
+                  self._check("point_kind", point_kind, torch.int32, (n_pts,), optional=True)]
+        rec = self.records.data_ptr() if self.relaid_ok else None
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            code = _native.lib().navi_observe(
+                d_ptr, e, int(azimuth_bins), int(elevation_bins), float(max_distance), float(structure_band_min),
+                float(structure_band_max), float(proximity_threshold), float(collision_clearance), outs[0],
+                outs[1], outs[2], rec, self.n_records if self.relaid_ok else 0,
+                self.relaid_table.data_ptr() if self.relaid_ok else None, self.n_scenes,
+                self.root_tables.data_ptr() if self.relaid_ok else None, pp[1], pp[0], n_pts, pp[2], pp[3],
+                pp[4], stream)
         _native.check(code)

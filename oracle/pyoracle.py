@@ -2,26 +2,38 @@
 
 TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 
-Functions and what pins each one (tests named in brackets):
+Functions and what pins each one (the pinning tests in brackets, ``tests/<file>::<test>``):
 
 * ``trace`` / ``trace_multi`` — restate ``projects/torch-sdf/cpp_src/kernel.cu:9-309``.
   Pinned by the ten known answers of ``projects/torch-sdf/tests/test_sphere_tracing.py:683-949``
-  [test_oracle_known_answers], hand-derived void exits and leaf accumulation,
-  the slab distance of ``projects/contracts/src/navi_contracts/testing/oracle_box.py:115-160``
-  and a cache-free brute-force march [test_oracle_properties].
-* ``point_query`` — build-defined clearance query (no reference kernel), pinned
-  against a pure-Python descent and closed forms [test_oracle_properties].
-* ``half_to_float`` / ``float_to_half`` — IEEE binary16, pinned exhaustively
-  against numpy's float16 [test_oracle_half]. ``float_to_half(quirk=True)`` restates
-  ``projects/voxel-dag/src/compiler.cpp:542-560``, pinned by hand-derived bit patterns.
-* ``compile_dense`` — restates ``compiler.cpp:563-674``, pinned by hand-built DAGs of
-  tiny grids and the reference's contract tests [test_oracle_compiler].
+  [test_oracle_tracer::test_known_answers], hand-derived void exits and leaf accumulation
+  [::test_void_cell_exit_closed_form, ::test_leaf_accumulation_closed_form], the slab distance of
+  ``projects/contracts/src/navi_contracts/testing/oracle_box.py:115-160``
+  [::test_unit_box_rays_within_reference_tolerance] and a cache-free brute-force march
+  [::test_cache_free_march_agrees_off_faces]; a planted mistake must fail them
+  [::test_planted_mistake_is_caught].
+* ``point_query`` — build-defined clearance query (no reference kernel), pinned against a
+  pure-Python descent and closed forms [test_oracle_tracer::test_point_query_matches_python_descent].
+* ``half_to_float`` / ``float_to_half`` — IEEE binary16, pinned exhaustively against numpy's
+  float16 [test_oracle_codecs::test_half_decode_exhaustive, ::test_half_encode_rne_matches_numpy].
+  ``float_to_half(quirk=True)`` restates ``projects/voxel-dag/src/compiler.cpp:542-560``, pinned by
+  hand-derived bit patterns [test_oracle_codecs::test_reference_quirk_encoder].
+* ``compile_dense`` — restates ``compiler.cpp:563-674``, pinned by hand-built DAGs of tiny grids
+  and the reference's contract tests [test_compiler::test_two_voxel_grid_by_hand and neighbours].
 * ``ray_directions`` / ``yaw_rotate`` — restate ``projects/environment/src/navi_environment/
-  backends/sdfdag_backend.py:205-221,1300-1310``; pinned by the cardinal directions, unit
-  norms, poles and index map of ``projects/environment/tests/unit/test_ray_direction_oracle.py``
-  [test_oracle_rays]. Exact float32 bits of numpy's sin/cos are parity unpinned (atol 1e-6).
-* ``postprocess`` — restates ``sdfdag_backend.py:408-473``; pinned by the known values of
-  ``projects/environment/tests/unit/test_postprocessing_oracle.py`` [test_oracle_postpass].
+  backends/sdfdag_backend.py:205-221,1300-1310``; pinned by the cardinal directions, unit norms,
+  poles and index map of ``projects/environment/tests/unit/test_ray_direction_oracle.py``
+  [test_caller_side::test_cardinal_directions and neighbours]. Exact float32 bits of numpy's
+  sin/cos are parity unpinned (atol 1e-6).
+* ``postprocess`` / ``fp16_depth_obs`` — restate ``sdfdag_backend.py:408-473``; pinned by the known
+  values of ``projects/environment/tests/unit/test_postprocessing_oracle.py`` and the horizon cases
+  of ``test_sdfdag_conventions.py:604-730`` [test_caller_side::test_postpass_known_values,
+  ::test_postpass_horizon_cases]. torch CPU ``log1p`` bits versus the reference's CUDA ``log1p``
+  are parity unpinned (atol 1e-6 in the reference's tests).
+* ``observation_ratios`` / ``observe`` — restate ``sdfdag_backend.py:366-405`` and the collision
+  test of ``:1340``; pinned by the known answer of ``test_sdfdag_conventions.py:123-142`` and
+  counts built by hand [test_caller_side::test_observation_ratios_known_answer,
+  ::test_observation_ratios_by_hand].
 """
 
 from __future__ import annotations
@@ -49,6 +61,8 @@ __all__ = [
     "yaw_rotate",
     "postprocess",
     "fp16_depth_obs",
+    "observation_ratios",
+    "observe",
 ]
 
 HIT_EPSILON = 0.01  # kernel.cuh:7
@@ -307,6 +321,49 @@ def fp16_depth_obs(out_distances, az_bins: int, el_bins: int, max_distance: floa
     depth = postprocess(out_distances, np.zeros(np.shape(out_distances), np.int32), az_bins,
                         el_bins, max_distance)[0]
     return depth.permute(0, 2, 1).unsqueeze(1).contiguous().numpy().astype(np.float16)
+
+
+def observation_ratios(clamped, valid, max_distance: float, band_min: float, band_max: float,
+                       proximity: float) -> np.ndarray:
+    """``_compute_observation_ratios_tensor`` (sdfdag_backend.py:366-405) on ``(B, Az, El)``
+    clamped distances and validity: ``[B, 4]`` float32 = starvation, proximity,
+    structure-band and forward-structure ratios. Python-float thresholds are rounded to
+    float32 before comparing, as torch does with scalars; means are float32 count / size."""
+    c = np.asarray(clamped, dtype=np.float32)
+    v = np.asarray(valid, dtype=bool)
+    b, az, el = c.shape
+    with np.errstate(invalid="ignore"):
+        sat = c >= np.float32(max_distance - 1e-3)
+        out = np.zeros((b, 4), np.float32)
+        out[:, 0] = sat.reshape(b, -1).sum(1).astype(np.float32) / np.float32(az * el)
+        if band_max > band_min:
+            band = v & (c >= np.float32(band_min)) & (c <= np.float32(band_max))
+            out[:, 2] = band.reshape(b, -1).sum(1).astype(np.float32) / np.float32(az * el)
+            half = max(1, az // 6)
+            sector = np.concatenate((band[:, :half, :], band[:, az - half:, :]), axis=1)
+            out[:, 3] = sector.reshape(b, -1).sum(1).astype(np.float32) / np.float32(2 * half * el)
+        if proximity > 0.0:
+            near = v & (c <= np.float32(proximity))
+            out[:, 1] = near.reshape(b, -1).sum(1).astype(np.float32) / np.float32(az * el)
+    return np.clip(out, 0.0, 1.0)
+
+
+def observe(out_distances, az_bins: int, el_bins: int, max_distance: float, band_min: float = 1.5,
+            band_max: float = 30.0, proximity: float = 2.0, clearance: float = 0.15) -> dict[str, np.ndarray]:
+    """The observation step after a trace: ``depth16 (B, 1, El, Az)`` float16 (north-star
+    layout of ``postprocess``'s depth), ``stats [B, 5]`` = min clamped distance and the four
+    ``observation_ratios``, ``collision [B]`` = min < clearance (sdfdag_backend.py:1340)."""
+    d = np.asarray(out_distances, dtype=np.float32)
+    depth, _, valid, min_d, clamped = postprocess(d, np.zeros(d.shape, np.int32), az_bins, el_bins, max_distance)
+    ratios = observation_ratios(clamped.numpy(), valid.numpy(), max_distance, band_min, band_max, proximity)
+    stats = np.concatenate([min_d.numpy()[:, None].astype(np.float32), ratios], axis=1)
+    with np.errstate(invalid="ignore"):
+        collision = (stats[:, 0] < np.float32(clearance)).astype(np.int32)
+    return {
+        "depth16": depth.permute(0, 2, 1).unsqueeze(1).contiguous().numpy().astype(np.float16),
+        "stats": stats,
+        "collision": collision,
+    }
 
 
 if os.environ.get("NAVI_ORACLE_EAGER"):

@@ -203,7 +203,7 @@ def _walk(rec, root, cell):
         b = 3 - lvl
         oct_ = ((ix >> b) & 1) | ((iy >> b) & 1) << 1 | ((iz >> b) & 1) << 2
         slot = int(rec[r][oct_]) if r < rec.shape[0] else 0x7FFFFFFE
-        if slot >= 0x7FFFFFFE or lvl == 3:
+        if slot >= 0x7FFFFFFD or lvl == 3:
             return slot, lvl + 1
         r = slot
 
@@ -223,7 +223,7 @@ def test_root_table_matches_record_walks(case):
     else:
         rec, root, _ = _native.relayout(np.array([(1 << 63) | (3 << 16) | 0x3C00], np.uint64))
     if case == "offset":  # the scene sits at record 7 of a pool
-        rec = np.concatenate([np.full((7, 8), 0x7FFFFFFF, np.uint32), np.where(rec < 0x7FFFFFFE, rec + 7, rec)])
+        rec = np.concatenate([np.full((7, 8), 0x7FFFFFFF, np.uint32), np.where(rec < 0x7FFFFFFD, rec + 7, rec)])
         root += 7
     table = _native.root_table(rec, root)
     slots = table & 0xFFFFFFFF
@@ -236,7 +236,7 @@ def test_root_table_matches_record_walks(case):
     if case == "one_leaf":
         assert set(depths.tolist()) == {0} and set(slots.tolist()) == {root}
     if case in ("room", "offset"):
-        assert (depths == 4).any() and (slots[depths == 4] < 0x7FFFFFFE).any()
+        assert (depths == 4).any() and (slots[depths == 4] < 0x7FFFFFFD).any()
 
 
 def _longest_chain(rec, root):
@@ -255,7 +255,7 @@ def _longest_chain(rec, root):
         best = 0
         for s in rec[r]:
             s = int(s)
-            if s < 0x7FFFFFFE:
+            if s < 0x7FFFFFFD:
                 best = max(best, h(s) + 1)
         on_path.discard(r)
         return best

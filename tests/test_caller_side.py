@@ -88,3 +88,54 @@ def test_fp16_observation_layout():
     assert obs.shape == (2, 1, 4, 8) and obs.dtype == np.float16
     ref = (torch.log1p(torch.from_numpy(d).clamp(0, 30)) / math.log1p(30.0)).reshape(2, 8, 4)
     np.testing.assert_allclose(obs[:, 0].astype(np.float32), ref.permute(0, 2, 1).numpy(), atol=1e-3)
+
+
+def test_postpass_horizon_cases():
+    """projects/environment/tests/unit/test_sdfdag_conventions.py:604-730: readings past
+    the horizon clamp to depth 1 and stay valid, the horizon itself is depth 1, negative
+    (inside-solid) readings clamp to depth 0."""
+    depth, _, valid, _, _ = oracle.postprocess(np.array([[5.0, 25.0]], np.float32), np.array([[1, 2]], np.int32),
+                                               2, 1, 10.0)
+    np.testing.assert_allclose(depth.reshape(-1).numpy(), [math.log1p(5.0) / math.log1p(10.0), 1.0], rtol=1e-6)
+    assert valid.reshape(-1).tolist() == [True, True]
+    depth, *_ = oracle.postprocess(np.array([[10.0]], np.float32), np.array([[3]], np.int32), 1, 1, 10.0)
+    assert float(depth.reshape(-1)[0]) == 1.0
+    depth, *_ = oracle.postprocess(np.array([[-0.25]], np.float32), np.array([[9]], np.int32), 1, 1, 10.0)
+    assert float(depth.reshape(-1)[0]) == 0.0
+
+
+def test_observation_ratios_known_answer():
+    """test_sdfdag_conventions.py:123-142: one of four pixels each starved (30 >= 20 - 1e-3),
+    near (0.6 <= 1.0) and in the structure band [1.5, 10] (3.0), forward sector = both bins."""
+    metric = np.array([[30.0, 0.6], [3.0, 15.0]], np.float32)[None]
+    clamped = np.clip(metric, 0.0, 20.0)
+    r = oracle.observation_ratios(clamped, np.ones_like(metric, bool), 20.0, 1.5, 10.0, 1.0)
+    np.testing.assert_allclose(r[0], [0.25, 0.25, 0.25, 0.25])
+    obs = oracle.observe(metric.reshape(1, 4), 2, 2, 20.0, band_min=1.5, band_max=10.0, proximity=1.0,
+                         clearance=0.7)
+    np.testing.assert_allclose(obs["stats"][0], [0.6, 0.25, 0.25, 0.25, 0.25])
+    assert obs["collision"].tolist() == [1]
+
+
+def test_observation_ratios_by_hand():
+    """Counts written out cell by cell: 12 azimuth bins x 3 elevations, max 10; the forward
+    sector is azimuth bins {0, 1, 10, 11} (12 // 6 = 2 on each side)."""
+    az, el = 12, 3
+    m = np.full((az, el), 5.0, np.float32)  # in band [1.5, 8], not near, not starved
+    m[0, 0] = 0.2                            # near (<= 0.5), not in band
+    m[11, 2] = 9.9995                        # starved (>= 9.999) and out of band
+    m[5, 1] = np.inf                         # starved after clamping, invalid
+    m[6, 1] = np.nan                         # invalid, nothing
+    obs = oracle.observe(m.reshape(1, -1), az, el, 10.0, band_min=1.5, band_max=8.0, proximity=0.5, clearance=0.15)
+    band = az * el - 4
+    fwd_band = 4 * el - 2
+    want = [np.nan, 2 / 36, 1 / 36, band / 36, fwd_band / (4 * el)]
+    np.testing.assert_allclose(obs["stats"][0, 1:], want[1:], rtol=1e-6)
+    assert np.isnan(obs["stats"][0, 0]) and obs["collision"].tolist() == [0]
+    m[6, 1] = 3.0
+    obs = oracle.observe(m.reshape(1, -1), az, el, 10.0, band_min=1.5, band_max=8.0, proximity=0.5, clearance=0.25)
+    assert float(obs["stats"][0, 0]) == np.float32(0.2) and obs["collision"].tolist() == [1]
+    # one azimuth bin: the first and last sixth are the same bin, counted twice (torch.cat)
+    one = oracle.observe(np.array([[2.0, 20.0]], np.float32), 1, 2, 30.0, band_min=1.5, band_max=8.0)
+    assert float(one["stats"][0, 4]) == 0.5
+    assert one["depth16"].shape == (1, 1, 2, 1)

@@ -286,3 +286,22 @@ def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
     d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
     ref = _oracle_multi([words] * 2, narrow, env_scene, o, d, 64, 5.0)
     _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, "narrow")
+
+
+@pytest.mark.parametrize("n", [31, 32])
+def test_bad_child_index_at_the_descent_limit(gpu, n):
+    """A child index past the array faults only when the descent examines the
+    child: at depth 31 (chain of 31 nodes) the ray reports NaN, at depth 32
+    (chain of 32) the 32-level limit comes first and the result is stale."""
+    from navi_amd.multiscene import ResidentScenes
+    from tests.test_boundary import _chain_words
+
+    words = _chain_words(n)
+    words[2 * n - 1] = words.size + 5  # the last node's child index
+    res = ResidentScenes([(words, [0, 0, 0], [1, 1, 1])])
+    o = np.array([[[1, 1, 1], [1, 1, 1], [0.2, 0.9, 0.4]]], np.float32)
+    d = np.array([[[-1, 0, 0], [0, 0, -1], [0, 1, 0]]], np.float32)
+    ref = oracle.trace(words, o, d, 6, 4.0, [0, 0, 0], [1, 1, 1])
+    assert np.isnan(ref["distance"][0, 0]) == (n == 31)
+    for kernel in ("raw", "relaid"):
+        _compare(_run(res, np.zeros(1, np.int32), o, d, 6, 4.0, kernel=kernel), ref, 4.0, f"badchild{n}/{kernel}")

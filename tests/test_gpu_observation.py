@@ -1,0 +1,226 @@
+"""GPU parity of the observation-step entry points against the CPU oracle:
+rays generated from poses in the tracer (navi_trace_relaid_poses), point-SDF
+queries (navi_point_query) and the fused post-pass (navi_observe).
+
+Bars: traced rays as in test_gpu_multiscene (bit-exact); point queries
+bit-exact (distance bits, semantic, kind); post-pass min distance and
+collision exact, ratios within 1e-6, fp16 depth within one binary16 ulp
+(torch CPU log1p versus the device's log1pf).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.test_gpu_multiscene import _compare, _corpus, _oracle_multi, _run
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def corpus():
+    return _corpus()
+
+
+def _resident(corpus):
+    from navi_amd.multiscene import ResidentScenes
+
+    return ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+
+
+def _poses(corpus, n_envs, seed):
+    rng = np.random.default_rng(seed)
+    env_scene = rng.integers(0, len(corpus), n_envs).astype(np.int32)
+    pos = np.empty((n_envs, 3), np.float32)
+    for s in range(len(corpus)):
+        idx = np.flatnonzero(env_scene == s)
+        if idx.size:
+            pos[idx] = corpus[s].free_origins(rng, idx.size)
+    yaw = rng.uniform(-math.pi, 3 * math.pi, n_envs).astype(np.float32)
+    rot = np.stack([np.cos(yaw), np.sin(yaw)], axis=1).astype(np.float32)
+    return env_scene, pos, rot
+
+
+def _rotate(local, rot):
+    """x' = x c + z s, y' = y, z' = (-x) s + z c with float32 rounding after each
+    operation (sdfdag_backend.py:1300-1310 in eager tensor code)."""
+    c = rot[:, None, 0:1]
+    s = rot[:, None, 1:2]
+    x, y, z = local[None, :, 0:1], local[None, :, 1:2], local[None, :, 2:3]
+    d = np.concatenate([x * c + z * s, np.broadcast_to(y, (rot.shape[0],) + y.shape[1:]), (-x) * s + z * c], -1)
+    return np.ascontiguousarray(d, np.float32)
+
+
+@pytest.mark.parametrize("az,el", [(32, 16), (24, 5)])
+def test_pose_rays_equal_explicit_rays(gpu, corpus, az, el):
+    import torch
+
+    res = _resident(corpus)
+    env_scene, pos, rot = _poses(corpus, 20, seed=az)
+    local = oracle.ray_directions(az, el)
+    dirs = _rotate(local, rot)
+    origins = np.ascontiguousarray(np.broadcast_to(pos[:, None, :], dirs.shape))
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, origins, dirs, 160, 30.0)
+    dev = res.device
+    t = {k: torch.from_numpy(v).to(dev) for k, v in
+         (("es", env_scene), ("local", local), ("pos", pos), ("rot", rot))}
+    out_d = torch.full((20, az * el), -7.0, device=dev)
+    out_s = torch.full((20, az * el), -7, device=dev, dtype=torch.int32)
+    out_n = torch.full((20, az * el), -7, device=dev, dtype=torch.int32)
+    res.cast_rays_poses(t["es"], t["local"], t["pos"], t["rot"], out_d, out_s, 160, 30.0, out_steps=out_n,
+                        elevation_bins=el)
+    torch.cuda.synchronize()
+    got = (out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), None)
+    _compare(got, ref, 30.0, f"poses/{az}x{el}")
+    explicit = _run(res, env_scene, origins, dirs, 160, 30.0, elevation_bins=el)
+    assert np.array_equal(explicit[0].view(np.uint32), got[0].view(np.uint32))
+
+
+def _point_cases(corpus, n, seed):
+    rng = np.random.default_rng(seed)
+    scene = rng.integers(0, len(corpus), n).astype(np.int32)
+    lo = np.array([corpus[s].bbox_min_list for s in scene], np.float64)
+    hi = np.array([corpus[s].bbox_max for s in scene], np.float64)
+    pts = rng.uniform(lo - 0.5, hi + 0.5, (n, 3)).astype(np.float32)
+    pts[: n // 8] = lo[: n // 8].astype(np.float32)  # on the lower domain faces
+    pts[n // 8: n // 4] = hi[n // 8: n // 4].astype(np.float32)  # on the upper faces (inclusive)
+    return scene, pts
+
+
+def _point_oracle(words_by_scene, bounds, scene, pts):
+    d = np.empty(len(pts), np.float32)
+    s = np.empty(len(pts), np.int32)
+    k = np.empty(len(pts), np.int32)
+    for sc in np.unique(scene):
+        idx = np.flatnonzero(scene == sc)
+        r = oracle.point_query(words_by_scene[sc], pts[idx], bounds[sc][:3], bounds[sc][3:])
+        d[idx], s[idx], k[idx] = r["distance"], r["semantic"], r["kind"]
+    return d, s, k
+
+
+def _same_bits(a, b):
+    return np.array_equal(a.view(np.uint32), b.view(np.uint32)) or np.array_equal(
+        np.where(np.isnan(a), np.float32(np.nan), a).view(np.uint32),
+        np.where(np.isnan(b), np.float32(np.nan), b).view(np.uint32))
+
+
+def test_point_queries(gpu, corpus):
+    import torch
+
+    from tests.test_boundary import _chain_words
+
+    chain = _chain_words(33)
+    bad = _chain_words(32)
+    bad[63] = bad.size + 5
+    leaf = np.array([(1 << 63) | (7 << 16) | 0x3C00], np.uint64)
+    scenes = [(c.words, c.bbox_min_list, c.bbox_max) for c in corpus]
+    scenes += [(chain, [0, 0, 0], [1, 1, 1]), (bad, [0, 0, 0], [1, 1, 1]), (leaf, [-1, -1, -1], [1, 1, 1])]
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes(scenes)
+    bounds = [list(s[1]) + list(s[2]) for s in scenes]
+    scene, pts = _point_cases(corpus, 3000, seed=12)
+    extra = np.array([[1, 1, 1], [0.999, 0.999, 0.999], [0.3, 0.2, 0.9]], np.float32)
+    for sc in (4, 5, 6):
+        scene = np.concatenate([scene, np.full(3, sc, np.int32)])
+        pts = np.concatenate([pts, extra])
+    want = _point_oracle([s[0] for s in scenes], bounds, scene, pts)
+    assert {0, 1, 2, 3}.issubset(set(want[2].tolist()))
+    dev = res.device
+    tp = torch.from_numpy(pts).to(dev)
+    ts = torch.from_numpy(scene).to(dev)
+    out_d = torch.full((len(pts),), -7.0, device=dev)
+    out_s = torch.full((len(pts),), -7, device=dev, dtype=torch.int32)
+    out_k = torch.full((len(pts),), -7, device=dev, dtype=torch.int32)
+    res.point_query(tp, out_d, out_s, point_scene=ts, out_kind=out_k)
+    torch.cuda.synchronize()
+    assert np.array_equal(out_k.cpu().numpy(), want[2])
+    assert np.array_equal(out_s.cpu().numpy(), want[1])
+    assert _same_bits(out_d.cpu().numpy(), want[0])
+    # unknown scene ids: NaN, kind 4
+    ts_bad = torch.tensor([-1, 99], dtype=torch.int32, device=dev)
+    tp2 = torch.zeros((2, 3), device=dev)
+    d2, s2, k2 = (torch.zeros(2, device=dev), torch.zeros(2, device=dev, dtype=torch.int32),
+                  torch.zeros(2, device=dev, dtype=torch.int32))
+    res.point_query(tp2, d2, s2, point_scene=ts_bad, out_kind=k2)
+    torch.cuda.synchronize()
+    assert torch.isnan(d2).all() and k2.tolist() == [4, 4] and s2.tolist() == [0, 0]
+
+
+def _observe_oracle_check(got, want):
+    d16, stats, coll = got
+    assert np.array_equal(coll, want["collision"])
+    assert _same_bits(stats[:, 0].copy(), want["stats"][:, 0].copy())
+    np.testing.assert_allclose(stats[:, 1:], want["stats"][:, 1:], atol=1e-6, rtol=0)
+    a = d16.astype(np.float32)
+    b = want["depth16"].astype(np.float32)
+    assert np.array_equal(np.isnan(a), np.isnan(b))
+    ulp = np.spacing(np.abs(np.nan_to_num(b)).astype(np.float16)).astype(np.float32)
+    assert (np.abs(np.nan_to_num(a) - np.nan_to_num(b)) <= ulp).all()
+
+
+@pytest.mark.parametrize("az,el,band", [(256, 48, (1.5, 30.0)), (12, 3, (1.5, 8.0)), (7, 5, (3.0, 3.0))])
+def test_observe_matches_oracle(gpu, corpus, az, el, band):
+    import torch
+
+    res = _resident(corpus)
+    rng = np.random.default_rng(az + el)
+    e = 9
+    d = rng.uniform(-1.0, 40.0, (e, az * el)).astype(np.float32)
+    d[0, :5] = [np.inf, -np.inf, 0.0, 30.0, 29.999]
+    d[1, 7] = np.nan
+    d[2] = rng.uniform(0.0, 0.3, az * el)  # a collision
+    want = oracle.observe(d, az, el, 30.0, band[0], band[1], 2.0, 0.15)
+    dev = res.device
+    td = torch.from_numpy(d).to(dev)
+    d16 = torch.empty((e, 1, el, az), dtype=torch.float16, device=dev)
+    st = torch.empty((e, 5), device=dev)
+    co = torch.empty((e,), dtype=torch.int32, device=dev)
+    res.observe(td, az, el, 30.0, structure_band_min=band[0], structure_band_max=band[1], out_depth_f16=d16,
+                out_stats=st, out_collision=co)
+    torch.cuda.synchronize()
+    _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
+
+
+def test_observation_step_end_to_end(gpu, corpus):
+    """Poses -> traced rays -> fused post-pass with point queries, against the oracle
+    pipeline on the same inputs."""
+    import torch
+
+    res = _resident(corpus)
+    az, el, e = 64, 16, 12
+    env_scene, pos, rot = _poses(corpus, e, seed=77)
+    local = oracle.ray_directions(az, el)
+    dirs = _rotate(local, rot)
+    origins = np.ascontiguousarray(np.broadcast_to(pos[:, None, :], dirs.shape))
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, origins, dirs, 128, 30.0)
+    want = oracle.observe(ref["distance"], az, el, 30.0)
+    rng = np.random.default_rng(3)
+    pts = (np.repeat(pos, 4, axis=0) + rng.uniform(-0.3, 0.3, (4 * e, 3))).astype(np.float32)
+    pscene = np.repeat(env_scene, 4).astype(np.int32)
+    pwant = _point_oracle([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus], pscene, pts)
+    dev = res.device
+    t = {k: torch.from_numpy(v).to(dev) for k, v in
+         (("es", env_scene), ("local", local), ("pos", pos), ("rot", rot), ("pts", pts), ("ps", pscene))}
+    out_d = torch.empty((e, az * el), device=dev)
+    out_s = torch.empty((e, az * el), device=dev, dtype=torch.int32)
+    res.cast_rays_poses(t["es"], t["local"], t["pos"], t["rot"], out_d, out_s, 128, 30.0, elevation_bins=el)
+    d16 = torch.empty((e, 1, el, az), dtype=torch.float16, device=dev)
+    st = torch.empty((e, 5), device=dev)
+    co = torch.empty((e,), dtype=torch.int32, device=dev)
+    pd = torch.empty((4 * e,), device=dev)
+    ps = torch.empty((4 * e,), device=dev, dtype=torch.int32)
+    pk = torch.empty((4 * e,), device=dev, dtype=torch.int32)
+    res.observe(out_d, az, el, 30.0, out_depth_f16=d16, out_stats=st, out_collision=co, points=t["pts"],
+                point_scene=t["ps"], point_distances=pd, point_semantics=ps, point_kind=pk)
+    torch.cuda.synchronize()
+    assert np.array_equal(out_d.cpu().numpy().view(np.uint32), ref["distance"].view(np.uint32))
+    _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
+    assert np.array_equal(pk.cpu().numpy(), pwant[2]) and np.array_equal(ps.cpu().numpy(), pwant[1])
+    assert _same_bits(pd.cpu().numpy(), pwant[0])
