@@ -78,6 +78,86 @@ def make_rays(corpus, n_envs, seed=4):
     return env_scene, origins, yaw, local
 
 
+def observation_steps(res, t_es, origins_env, yaw_env, E, args):
+    """The full observation step, repeated for seeded random-walk poses: trace rays
+    generated in the kernel from each env's pose, then one launch that packs the fp16
+    (env, 1, El, Az) depth, reduces per-env clearance / ratios / collision and answers 4
+    point-SDF queries per env (the proposed move and three probes jittered +-0.3 m). A
+    move is kept when the proposed point clears 0.15 m. Returns rays/s over the steps."""
+    import torch
+
+    from navi_amd import scenes as S
+
+    dev = res.device
+    steps = args.obs_steps
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    pos = torch.from_numpy(np.ascontiguousarray(origins_env, np.float32)).to(dev)
+    yaw = torch.from_numpy(np.asarray(yaw_env, np.float32)).to(dev)
+    local = torch.from_numpy(S.canonical_directions(AZ, EL)).to(dev)
+    dpos = torch.randn((steps, E, 3), generator=gen, device=dev) * 0.05
+    dyaw = torch.randn((steps, E), generator=gen, device=dev) * 0.1
+    jitter = torch.rand((steps, E, 3, 3), generator=gen, device=dev) * 0.6 - 0.3
+    pscene = t_es.repeat_interleave(4)
+    rot = torch.empty((E, 2), device=dev)
+    pts = torch.empty((E, 4, 3), device=dev)
+    R = AZ * EL
+    out_d = torch.empty((E, R), device=dev)
+    out_s = torch.empty((E, R), device=dev, dtype=torch.int32)
+    d16 = torch.empty((E, 1, EL, AZ), device=dev, dtype=torch.float16)
+    stats = torch.empty((E, 5), device=dev)
+    coll = torch.empty((E,), device=dev, dtype=torch.int32)
+    pd = torch.empty((4 * E,), device=dev)
+    ps = torch.empty((4 * E,), device=dev, dtype=torch.int32)
+    pk = torch.empty((4 * E,), device=dev, dtype=torch.int32)
+
+    def observe():
+        res.observe(out_d, AZ, EL, args.max_distance, out_depth_f16=d16, out_stats=stats, out_collision=coll,
+                    points=pts.view(-1, 3), point_scene=pscene, point_distances=pd, point_semantics=ps,
+                    point_kind=pk)
+
+    def one(k):
+        torch.stack((torch.cos(yaw), torch.sin(yaw)), 1, out=rot)
+        res.cast_rays_poses(t_es, local, pos, rot, out_d, out_s, args.max_steps, args.max_distance,
+                            elevation_bins=EL)
+        pts[:, 0] = pos + dpos[k]
+        pts[:, 1:] = pos[:, None, :] + jitter[k]
+        observe()
+        keep = pd.view(E, 4)[:, 0] >= 0.15
+        pos.copy_(torch.where(keep[:, None], pts[:, 0], pos))
+        yaw.add_(dyaw[k])
+
+    one(0)  # warm-up (the poses then start from step 1's state)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for k in range(steps):
+        one(k)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    moved = float((pd.view(E, 4)[:, 0] >= 0.15).float().mean().item())
+    ev0.record(stream)
+    for _ in range(20):
+        observe()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_observe = ev0.elapsed_time(ev1) / 20
+    return {
+        "workload": f"{E} envs x {AZ}x{EL} rays from poses, {steps} seeded random-walk steps "
+                    f"(dpos ~ N(0, 0.05 m), dyaw ~ N(0, 0.1 rad), move kept if its point SDF >= 0.15 m), "
+                    f"fp16 (env, 1, {EL}, {AZ}) depth + per-env stats + {4 * E} point queries per step",
+        "rays_per_s": round(E * R / (ms / 1e3), 1),
+        "ms_per_step": round(ms, 4),
+        "observe_launch_ms": round(ms_observe, 4),
+        "entry_points": ["navi_trace_relaid_poses", "navi_observe"],
+        "last_step_moves_kept": round(moved, 4),
+        "mean_min_distance": round(float(stats[:, 0].mean().item()), 4),
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +171,8 @@ def main() -> int:
     ap.add_argument("--cpu-envs", type=int, default=256, help="envs in the CPU-baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-raw", action="store_true", help="skip timing the reference-layout kernel")
+    ap.add_argument("--obs-steps", type=int, default=128,
+                    help="observation-step workload: steps of seeded random-walk poses (0 to skip)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run one device copy of this many MiB (known HBM bytes) so a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run can scale the tracer's counters")
@@ -222,6 +304,8 @@ def main() -> int:
             "bit_exact_distance": int(np.sum((gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both_nan)),
         }
 
+    obs = observation_steps(res, t_es, origins_env, yaw, E, args) if args.obs_steps > 0 else None
+
     traffic = None
     tp = Path(args.traffic_profile)
     if tp.exists():
@@ -266,6 +350,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "parity": parity,
+        "observation_step": obs,
         "scene_compile_s": round(t_compile, 2),
     }
     print(json.dumps(line), flush=True)
