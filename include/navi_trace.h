@@ -87,8 +87,11 @@ int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, in
  * record index. With out_records NULL only counts; otherwise writes up to
  * cap_records records. *root_slot is the root's slot value (0 = record 0, or
  * an inlined leaf). n_levels_prefix (optional, 8 entries) receives the number
- * of records at depth <= l. Returns NAVI_E_LAYOUT for DAGs with a reachable
- * leaf semantic above 0x7fff (trace those with navi_cast_rays*).
+ * of records at depth <= l. When no record lies deeper than 30 levels
+ * (navi_record_depth <= 30) every 0x7ffffffd slot is written as 0x7ffffffe:
+ * it is examined above the descent limit, where both fault. Returns
+ * NAVI_E_LAYOUT for DAGs with a reachable leaf semantic above 0x7fff (trace
+ * those with navi_cast_rays*).
  */
 int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
                   uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix);
@@ -104,7 +107,8 @@ typedef struct navi_relaid_scene {
     uint32_t root_slot;
     float bbox_min[3];
     float bbox_max[3];
-    uint32_t max_depth;   /* navi_record_depth of the scene; 0xffffffff if unknown */
+    uint32_t max_depth;   /* navi_record_depth of the scene's records as navi_relayout wrote
+                             them; 0xffffffff if unknown */
     uint32_t reserved;    /* 0 */
 } navi_relaid_scene;
 

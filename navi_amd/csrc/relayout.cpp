@@ -69,6 +69,52 @@ inline bool child_slot(const uint64_t* w, uint64_t n, uint32_t idx, std::vector<
 
 }  // namespace
 
+namespace {
+
+// Longest chain of internal records below `root` (the root at 0), or
+// 0xffffffff when a cycle or an out-of-range record is reachable.
+// Iterative depth-first search, O(records + slots).
+uint32_t longest_chain(const uint32_t* records, uint64_t n_records, uint32_t root) {
+    if (root >= kSlotBadChild) return 0;  // one-leaf DAG (or a void / fault root slot)
+    if (root >= n_records) return 0xffffffffu;
+    // height[r]: longest chain of records below r (0 = no internal child);
+    // kOpen marks a record on the current path (a revisit means a cycle).
+    constexpr uint32_t kUnseen = 0xffffffffu, kOpen = 0xfffffffeu;
+    std::vector<uint32_t> height(n_records, kUnseen);
+    struct Frame {
+        uint32_t rec;
+        uint32_t next;  // next octant to visit
+        uint32_t best;
+    };
+    std::vector<Frame> stack;
+    stack.push_back({root, 0u, 0u});
+    height[root] = kOpen;
+    while (!stack.empty()) {
+        Frame& f = stack.back();
+        if (f.next == 8u) {
+            height[f.rec] = f.best;
+            const uint32_t h = f.best;
+            stack.pop_back();
+            if (!stack.empty() && h + 1u > stack.back().best) stack.back().best = h + 1u;
+            continue;
+        }
+        const uint32_t slot = records[8ull * f.rec + f.next++];
+        if (slot >= kSlotBadChild) continue;  // leaf, void or fault slot
+        if (slot >= n_records) return 0xffffffffu;
+        const uint32_t h = height[slot];
+        if (h == kOpen) return 0xffffffffu;
+        if (h == kUnseen) {
+            height[slot] = kOpen;
+            stack.push_back({slot, 0u, 0u});
+        } else if (h + 1u > f.best) {
+            f.best = h + 1u;
+        }
+    }
+    return height[root];
+}
+
+}  // namespace
+
 extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records,
                              uint64_t cap_records, uint64_t* n_records, uint32_t* root_slot,
                              uint64_t* n_levels_prefix) {
@@ -130,6 +176,12 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
         for (int l = level; l < 8; ++l) n_levels_prefix[l] = queue.size();
     }
     *n_records = queue.size();
+    // When no record lies deeper than 30 levels every slot is examined above
+    // the 32-level limit, where a bad child index faults like a bad table word.
+    if (out_records && longest_chain(out_records, queue.size(), 0u) <= 30u) {
+        for (size_t k = 0; k < 8 * queue.size(); ++k)
+            if (out_records[k] == kSlotBadChild) out_records[k] = kSlotFault;
+    }
     return NAVI_OK;
 }
 
@@ -160,6 +212,7 @@ extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records
                 r = slot;
             }
         }
+        if (slot == kSlotBadChild) slot = kSlotFault;  // examined at depth <= 4: a fault
         out_table[c] = static_cast<uint64_t>(slot) | (static_cast<uint64_t>(d) << 32);
     }
     return NAVI_OK;
@@ -169,59 +222,11 @@ extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records
 // record reachable from root_slot sits at that depth (the root at 0). Records
 // hold record slots as indices into `records` (a pool). *max_depth is
 // 0xffffffff when a cycle or an out-of-range record is reachable, where the
-// descent limit of kernel.cu:136 decides results. Iterative depth-first
-// search, O(records + slots).
+// descent limit of kernel.cu:136 decides results.
 extern "C" int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
                                  uint32_t* max_depth) {
     using navi::set_error;
     if (!max_depth || (!records && n_records)) return set_error(NAVI_E_ARG, "null argument");
-    if (root_slot >= kSlotBadChild) {  // one-leaf DAG (or a void / fault root slot)
-        *max_depth = 0;
-        return NAVI_OK;
-    }
-    if (root_slot >= n_records) {
-        *max_depth = 0xffffffffu;
-        return NAVI_OK;
-    }
-    // height[r]: longest chain of records below r (0 = no internal child);
-    // kOpen marks a record on the current path (a revisit means a cycle).
-    constexpr uint32_t kUnseen = 0xffffffffu, kOpen = 0xfffffffeu;
-    std::vector<uint32_t> height(n_records, kUnseen);
-    struct Frame {
-        uint32_t rec;
-        uint32_t next;  // next octant to visit
-        uint32_t best;
-    };
-    std::vector<Frame> stack;
-    stack.push_back({root_slot, 0u, 0u});
-    height[root_slot] = kOpen;
-    while (!stack.empty()) {
-        Frame& f = stack.back();
-        if (f.next == 8u) {
-            height[f.rec] = f.best;
-            const uint32_t h = f.best;
-            stack.pop_back();
-            if (!stack.empty() && h + 1u > stack.back().best) stack.back().best = h + 1u;
-            continue;
-        }
-        const uint32_t slot = records[8ull * f.rec + f.next++];
-        if (slot >= kSlotBadChild) continue;  // leaf, void or fault slot
-        if (slot >= n_records) {
-            *max_depth = 0xffffffffu;
-            return NAVI_OK;
-        }
-        const uint32_t h = height[slot];
-        if (h == kOpen) {
-            *max_depth = 0xffffffffu;
-            return NAVI_OK;
-        }
-        if (h == kUnseen) {
-            height[slot] = kOpen;
-            stack.push_back({slot, 0u, 0u});
-        } else if (h + 1u > f.best) {
-            f.best = h + 1u;
-        }
-    }
-    *max_depth = height[root_slot];
+    *max_depth = longest_chain(records, n_records, root_slot);
     return NAVI_OK;
 }

@@ -185,7 +185,7 @@ __device__ __forceinline__ uint32_t plane_cell(float p, const float* pl, float& 
     return j0 + (up ? 1u : 0u);
 }
 
-template <bool kPlanes>
+template <bool kPlanes, bool kPoses>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
     extern __shared__ SceneLds lds_scenes[];
     float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 int32_t env;
                 ray = ray_of(P, q, env);
                 const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
-                if (P.local_dirs != nullptr) {
+                if (kPoses) {
                     // sdfdag_backend.py:1300-1312: origin = the env's position;
                     // x' = x c + z s, y' = y, z' = (-x) s + z c, each product
                     // and sum rounded on its own as in the eager tensor code
@@ -444,16 +444,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 cur_rec = slot;
                 descending = slot < kSlotBadChild && depth < kMaxDepth;
             }
+            // a bad child index faults only where the reference examines the
+            // child, above the 32-level limit; at depth 32 the result is stale
+            slot = (slot == kSlotBadChild && depth < kMaxDepth) ? kSlotFault : slot;
         }
 
         // ---- classify the query result and update the caches ----
-        const bool leaf_child = (slot & 0x80000000u) != 0u && (shallow || depth < kMaxDepth);  // examined at depth < 32
+        // (the shallow loop leaves `depth` at the table's value, <= 4: below the limit, as
+        // every slot of a shallow scene is)
+        const bool leaf_child = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at depth < 32
         const bool is_void = hit_vd || (!cached && slot == kSlotVoid);
         const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
-        // a bad child index faults only where the reference examines the
-        // child, above the 32-level limit; at depth 32 the result is stale
-        const bool is_fault = !cached && (slot == kSlotFault ||
-                                          (slot == kSlotBadChild && (shallow || depth < kMaxDepth)));
+        // (shallow scenes carry no bad-child slots: navi_relayout and the root
+        // table turn them into faults, which they are at every depth < 32)
+        const bool is_fault = !cached && slot == kSlotFault;
         const bool new_void = did_descend && is_void;
         const bool new_leaf = !cached && is_leaf;  // from a descent
         vd.x0 = new_void ? cur.x0 : vd.x0;
@@ -560,7 +564,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
 // to exactly that, so no wave waits for a slot and the sweep has no second,
 // partly empty round.
 // (per LDS size of the launch; guarded by g_queue_mu).
-std::map<std::pair<bool, size_t>, int> g_grid_blocks;
+std::map<std::pair<int, size_t>, int> g_grid_blocks;
 
 // Work-queue counters, one pair per (device, stream), allocated once per device
 // at its first launch (a 2 KiB device buffer, zeroed then). Launches on one
@@ -605,8 +609,10 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     const bool use_planes = P.n_scenes <= kPlaneScenes;
     const size_t lds = static_cast<size_t>(P.n_scenes) *
                        (sizeof(SceneLds) + (use_planes ? 3 * kPlaneStride * sizeof(float) : 0));
-    const auto kernel = use_planes ? trace_relaid_kernel<true> : trace_relaid_kernel<false>;
-    const auto key = std::make_pair(use_planes, lds);
+    const bool poses = P.local_dirs != nullptr;
+    const auto kernel = use_planes ? (poses ? trace_relaid_kernel<true, true> : trace_relaid_kernel<true, false>)
+                                   : (poses ? trace_relaid_kernel<false, true> : trace_relaid_kernel<false, false>);
+    const auto key = std::make_pair(2 * static_cast<int>(use_planes) + static_cast<int>(poses), lds);
     int grid_blocks = 0;
     {
         std::lock_guard<std::mutex> lock(g_queue_mu);

@@ -301,3 +301,18 @@ def test_record_depth(case):
         assert got == int(case[5:]) - 1
     if case == "shared":
         assert got == 2
+
+
+@pytest.mark.parametrize("n,kept", [(31, False), (32, True)])
+def test_relayout_resolves_bad_children_of_shallow_scenes(n, kept):
+    """A child index past the words is a fault wherever it is examined above the
+    32-level limit: in a graph at most 30 records deep that is everywhere, so the
+    relayout writes it as a plain fault; deeper graphs keep the distinct code."""
+    words = _chain_words(n)
+    words[2 * n - 1] = words.size + 5
+    rec, root, _ = _native.relayout(words)
+    assert _native.record_depth(rec, root) == n - 1
+    assert bool((rec == 0x7FFFFFFD).any()) == kept
+    assert bool((rec == 0x7FFFFFFE).any()) == (not kept)
+    table = _native.root_table(rec, root)
+    assert not ((table & 0xFFFFFFFF) == 0x7FFFFFFD).any()
