@@ -22,8 +22,10 @@
 // Arithmetic: the void-cell exit divides (kernel.cu:54-85) use a per-ray
 // correctly rounded reciprocal and one Markstein correction,
 // q = fma(fma(-a*r, b, a), r, a*r), which equals the IEEE quotient a/b when
-// r = RN(1/b) and nothing over/underflows (|a| in [2^-60, 2^60], |b| in
-// [1e-4, 2^20]); other operands take the IEEE division. 32-bit work indexing with
+// r = RN(1/b) and nothing over/underflows. Only quotients of at least 1e-5
+// can reach the result (the exit is clamped below at 1e-5), and for those,
+// with |b| > 1e-4 and box coordinates below 2^100, every intermediate is a
+// normal number; launches with larger coordinates take the IEEE division. 32-bit work indexing with
 // multiply-high division by the (uniform) rays-per-env and tile counts.
 #include <hip/hip_runtime.h>
 
@@ -117,16 +119,11 @@ __device__ __forceinline__ uint32_t ray_of(const RelaidParams& P, uint32_t q, in
 }
 
 // a / b for the exit distance: Markstein-corrected product with r = RN(1/b);
-// equal to the IEEE quotient when div_safe(a, b) (no over/underflow anywhere).
+// equal to the IEEE quotient when nothing over/underflows. NaN when r is.
 __device__ __forceinline__ float markstein(float a, float b, float r) {
     const float q0 = a * r;
     const float e = __builtin_fmaf(-q0, b, a);
     return __builtin_fmaf(e, r, q0);
-}
-
-__device__ __forceinline__ bool div_safe(float a, float b) {
-    const float aa = fabsf(a), bb = fabsf(b);
-    return (aa >= 0x1p-60f && aa <= 0x1p60f && bb >= 0x1p-20f && bb <= 0x1p20f) || a == 0.0f;
 }
 
 constexpr uint32_t kRefillMin = 8;
@@ -189,22 +186,23 @@ template <bool kPlanes, bool kPoses>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
     extern __shared__ SceneLds lds_scenes[];
     float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
-    // `nested`: every scene box has coordinates below 2^126 in magnitude, so
-    // lo + hi never overflows, every split plane lies within its box and each
-    // descent box lies within its parent and the domain.
+    // `tame`: every scene box has coordinates below 2^100 in magnitude, so
+    // lo + hi never overflows, every split plane lies within its box, each
+    // descent box lies within its parent and the domain, and exit quotients
+    // (numerators below 2^101, divisors above 1e-4) stay far from overflow.
     // `shallow`: no record of any scene lies deeper than 30 levels, so every
     // slot a descent reads is at depth <= 31 and the 32-level limit of
     // kernel.cu:136 never applies.
-    int nested = 1, shallow = 1;
+    int tame = 1, shallow = 1;
     for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
         const navi_relaid_scene d = P.scenes[i];
         lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
                                  d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
         for (int a = 0; a < 3; ++a)
-            nested &= (fabsf(d.bbox_min[a]) < 0x1p126f && fabsf(d.bbox_max[a]) < 0x1p126f) ? 1 : 0;
+            tame &= (fabsf(d.bbox_min[a]) < 0x1p100f && fabsf(d.bbox_max[a]) < 0x1p100f) ? 1 : 0;
         shallow &= d.max_depth <= static_cast<uint32_t>(kMaxDepth - 2) ? 1 : 0;
     }
-    nested = __syncthreads_and(nested);
+    tame = __syncthreads_and(tame);
     shallow = __syncthreads_and(shallow);
     // `planes`: every scene's depth-4 cells can be located from its planes
     int planes = kPlanes ? 1 : 0;
@@ -217,7 +215,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         planes = __syncthreads_and(planes);
     }
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
     // Static schedule: this wave's chunks are wave, wave + n_waves, ...
     const uint32_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0u;
@@ -300,9 +298,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     dy = P.dirs[3 * ray + 1];
                     dz = P.dirs[3 * ray + 2];
                 }
-                rx = 1.0f / dx;  // correctly rounded (IEEE division)
-                ry = 1.0f / dy;
-                rz = 1.0f / dz;
+                // correctly rounded reciprocals (IEEE division) of the axes the
+                // exit uses (|d| > 1e-4, kernel.cu:54-85); NaN marks the others,
+                // whose quotients fminf then ignores
+                rx = (dx > kDirEps || dx < -kDirEps) ? 1.0f / dx : __builtin_nanf("");
+                ry = (dy > kDirEps || dy < -kDirEps) ? 1.0f / dy : __builtin_nanf("");
+                rz = (dz > kDirEps || dz < -kDirEps) ? 1.0f / dz : __builtin_nanf("");
                 t = 0.f;
                 dist = 0.f;
                 sem = 0;
@@ -478,25 +479,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
 
         // ---- finish the step (kernel.cu:297-308) ----
         // kernel.cu:54-85 on the void box, branch-free: the face per axis is
-        // fixed by the direction's sign; the Markstein quotient is exact unless
-        // an operand is out of its safe range, which takes the IEEE division.
-        const bool ax = dx > kDirEps || dx < -kDirEps;
-        const bool ay = dy > kDirEps || dy < -kDirEps;
-        const bool az = dz > kDirEps || dz < -kDirEps;
+        // fixed by the direction's sign; axes with |d| <= 1e-4 have a NaN
+        // reciprocal and drop out of the minimum.
         const float nx = (dx > 0.f ? vd.x1 : vd.x0) - px;
         const float ny = (dy > 0.f ? vd.y1 : vd.y0) - py;
         const float nz = (dz > 0.f ? vd.z1 : vd.z0) - pz;
-        float qx = markstein(nx, dx, rx), qy = markstein(ny, dy, ry), qz = markstein(nz, dz, rz);
-        const bool safe = (!ax || div_safe(nx, dx)) && (!ay || div_safe(ny, dy)) && (!az || div_safe(nz, dz));
-        if (!safe && is_void) {
-            qx = nx / dx;
-            qy = ny / dy;
-            qz = nz / dz;
+        float e;
+        if (tame) {
+            e = fminf(fminf(fminf(markstein(nx, dx, rx), markstein(ny, dy, ry)), markstein(nz, dz, rz)),
+                      kOutsideDomain);
+        } else {
+            e = kOutsideDomain;
+            e = rx == rx ? fminf(e, nx / dx) : e;
+            e = ry == ry ? fminf(e, ny / dy) : e;
+            e = rz == rz ? fminf(e, nz / dz) : e;
         }
-        float e = kOutsideDomain;
-        e = ax ? fminf(e, qx) : e;
-        e = ay ? fminf(e, qy) : e;
-        e = az ? fminf(e, qz) : e;
         const float void_d = fmaxf(e, kVoidAdvanceEps);
         const float leaf_d = half_to_float(lf_slot & 0xffffu);
         const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
@@ -522,7 +519,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // used, so it cannot hit. Up to kLeafRun of them are taken here per
         // lane, far cheaper than a full step; the first point that leaves the
         // box is left to the next full step, which recomputes it.
-        // With nested boxes the first two tests cannot fire inside the leaf
+        // With tame boxes the first two tests cannot fire inside the leaf
         // box: it lies within the domain, and the cached void cell is another
         // terminal cell of the same tree, so the two differ on a split plane
         // with the leaf box on its closed side and the void interior strictly
@@ -533,7 +530,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             const float qy = __builtin_fmaf(t, dy, oy);
             const float qz = __builtin_fmaf(t, dz, oz);
             run = in_box(qx, qy, qz, lf);
-            if (!nested) {
+            if (!tame) {
                 const Box dm{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
                 run = run && !(vd_ok && in_box_strict(qx, qy, qz, vd)) && in_box(qx, qy, qz, dm);
             }
