@@ -158,6 +158,42 @@ def observation_steps(res, t_es, origins_env, yaw_env, E, args):
     }
 
 
+def dropin_timing(corpus, env_scene, t_o, t_d, args):
+    """The drop-in torch_sdf.cast_rays on one resident DAG (scene 0) for the envs that use
+    it: record-layout tracer (converted once per DAG tensor) versus the word-layout kernel."""
+    import torch
+
+    from navi_amd import torch_sdf
+
+    idx = torch.from_numpy(np.flatnonzero(env_scene == 0)).to(t_o.device)
+    o = t_o.index_select(0, idx).contiguous()
+    d = t_d.index_select(0, idx).contiguous()
+    sc = corpus[0]
+    dag = torch.from_numpy(sc.words.view(np.int64)).to(t_o.device)
+    out_d = torch.empty(o.shape[:2], device=t_o.device)
+    out_s = torch.empty(o.shape[:2], device=t_o.device, dtype=torch.int32)
+    result = {"envs": int(idx.numel()), "rays": int(o.shape[0] * o.shape[1]), "scene": sc.name}
+    for kernel, reps in (("auto", 10), ("raw", 2)):
+        def call():
+            torch_sdf.cast_rays(dag, o, d, out_d, out_s, args.max_steps, args.max_distance, sc.bbox_min_list,
+                                list(sc.bbox_max), args.resolution, True, elevation_bins=EL, kernel=kernel)
+        t0 = time.perf_counter()
+        call()  # auto: converts the DAG once
+        torch.cuda.synchronize()
+        first = time.perf_counter() - t0
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(reps):
+            call()
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / reps
+        result[kernel] = {"rays_per_s": round(result["rays"] / (ms / 1e3), 1), "ms": round(ms, 3),
+                          "first_call_s": round(first, 3)}
+    return result
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -305,6 +341,7 @@ def main() -> int:
         }
 
     obs = observation_steps(res, t_es, origins_env, yaw, E, args) if args.obs_steps > 0 else None
+    dropin = dropin_timing(corpus, env_scene, t_o, t_d, args) if args.obs_steps > 0 else None
 
     traffic = None
     tp = Path(args.traffic_profile)
@@ -351,6 +388,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "parity": parity,
         "observation_step": obs,
+        "dropin_cast_rays": dropin,
         "scene_compile_s": round(t_compile, 2),
     }
     print(json.dumps(line), flush=True)

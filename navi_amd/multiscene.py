@@ -28,7 +28,7 @@ class ResidentScenes:
     """
 
     def __init__(self, scenes: Sequence[tuple[np.ndarray, Sequence[float], Sequence[float]]],
-                 device: str | torch.device = "cuda") -> None:
+                 device: str | torch.device = "cuda", *, keep_words: bool = True) -> None:
         if not scenes:
             raise ValueError("at least one scene is required")
         self.device = torch.device(device)
@@ -53,7 +53,8 @@ class ResidentScenes:
         self.n_scenes = len(scenes)
         self.word_counts = [int(c.size) for c in chunks]
         self.host_table = table
-        self.pool = torch.from_numpy(np.concatenate(chunks).view(np.int64)).to(self.device)
+        # the word pool serves kernel="raw"; callers that keep their own word tensor skip it
+        self.pool = torch.from_numpy(np.concatenate(chunks).view(np.int64)).to(self.device) if keep_words else None
         self.table = torch.from_numpy(table.view(np.uint8).copy()).to(self.device)
 
         # device record layout (one 32-byte record per internal node)
@@ -97,7 +98,7 @@ class ResidentScenes:
 
     @property
     def pool_bytes(self) -> int:
-        return int(self.pool.numel()) * 8
+        return int(self.pool.numel()) * 8 if self.pool is not None else 0
 
     @property
     def record_bytes(self) -> int:
@@ -155,6 +156,8 @@ class ResidentScenes:
             return
         if kernel not in ("relaid", "raw"):
             raise ValueError(f"unknown kernel {kernel!r}")
+        if self.pool is None:
+            raise RuntimeError("this ResidentScenes keeps no word pool (keep_words=False)")
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
             code = _native.lib().navi_cast_rays_multi(

@@ -129,13 +129,18 @@ def cast_rays(
     *,
     hit_epsilon: float = _HIT_EPSILON,
     out_steps: Any | None = None,
+    elevation_bins: int = 0,
+    kernel: str = "auto",
 ) -> None:
     """Batched sphere tracing of a device-resident ``.gmdag`` DAG on the MI355X.
 
     Drop-in for ``torch_sdf.cast_rays`` (``backend.py:145-197``): writes every
     element of ``out_distances`` / ``out_semantics`` in place, asynchronously on
-    PyTorch's current stream. Keyword-only extensions: ``hit_epsilon`` and
-    ``out_steps`` (int32 ``[B, R]`` per-ray step counts). GPU only.
+    PyTorch's current stream. Keyword-only extensions: ``hit_epsilon``,
+    ``out_steps`` (int32 ``[B, R]`` per-ray step counts), ``elevation_bins``
+    (the rays are in the canonical ``az * El + el`` order with this ``El``) and
+    ``kernel`` (``"auto"``: record-layout tracer with a cached conversion of the
+    DAG tensor; ``"raw"``: the word-layout kernel). GPU only.
     """
     if not HAS_CUDA_BACKEND:
         raise RuntimeError(
@@ -158,6 +163,10 @@ def cast_rays(
         extra["hit_epsilon"] = hit_epsilon
     if out_steps is not None:
         extra["out_steps"] = out_steps
+    if elevation_bins:
+        extra["elevation_bins"] = int(elevation_bins)
+    if kernel != "auto":
+        extra["kernel"] = kernel
     backend.cast_rays(
         dag_tensor,
         origins,

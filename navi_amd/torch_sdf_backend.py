@@ -10,8 +10,19 @@ PyTorch's *current* HIP stream — the reference launches on the legacy default
 stream (``kernel.cu:320``) although its trainer calls it under side streams.
 
 Additions, all keyword-only so the positional contract is unchanged:
-``hit_epsilon`` (the reference's compile-time ``kHitEpsilon``, ``kernel.cuh:7``)
-and ``out_steps`` (an int32 ``[B, R]`` tensor receiving per-ray step counts).
+``hit_epsilon`` (the reference's compile-time ``kHitEpsilon``, ``kernel.cuh:7``),
+``out_steps`` (an int32 ``[B, R]`` tensor receiving per-ray step counts),
+``elevation_bins`` (declares the canonical ``az * El + el`` ray order so rays are
+traced in angular tiles) and ``kernel``.
+
+Kernels. ``kernel="auto"`` (default) traces with the record-layout tracer
+(``navi_trace_relaid``): the first call with a given DAG tensor copies its words
+to the host once, converts them (``navi_relayout``, ``navi_build_root_table``)
+and keeps the device copy, keyed by the tensor object, its version counter
+(in-place writes invalidate it) and the bbox. DAGs the record layout cannot
+hold (a leaf semantic above 0x7fff) and batches above 2^30 rays use the
+word-layout kernel (``navi_cast_rays``), as does ``kernel="raw"``. Results are
+identical either way.
 """
 
 from __future__ import annotations
@@ -21,6 +32,9 @@ from typing import Any
 
 import numpy as np
 import torch
+
+import threading
+import weakref
 
 from . import _native
 
@@ -112,6 +126,41 @@ def validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics
         _check(t.device == dev, f"{name} must be on the same device as dag_tensor ({dev})")
 
 
+class _RecordLayout:
+    """The record-layout copy of one DAG tensor (see the module docstring)."""
+
+    def __init__(self, dag_tensor: torch.Tensor, bounds: tuple[tuple[float, ...], tuple[float, ...]]) -> None:
+        from .multiscene import ResidentScenes
+
+        self.ref = weakref.ref(dag_tensor)
+        self.version = dag_tensor._version
+        self.data_ptr = dag_tensor.data_ptr()
+        self.bounds = bounds
+        words = dag_tensor.detach().cpu().numpy().view(np.uint64)
+        scenes = ResidentScenes([(words, bounds[0], bounds[1])], dag_tensor.device, keep_words=False)
+        self.scenes = scenes if scenes.relaid_ok else None
+
+    def valid_for(self, dag_tensor: torch.Tensor, bounds) -> bool:
+        return (self.ref() is dag_tensor and self.version == dag_tensor._version
+                and self.data_ptr == dag_tensor.data_ptr() and self.bounds == bounds)
+
+
+_layout_lock = threading.Lock()
+_layouts: dict[int, _RecordLayout] = {}
+
+
+def _record_layout(dag_tensor: torch.Tensor, bbox_min, bbox_max):
+    bounds = (tuple(_f32(v) for v in bbox_min), tuple(_f32(v) for v in bbox_max))
+    with _layout_lock:
+        entry = _layouts.get(id(dag_tensor))
+        if entry is None or not entry.valid_for(dag_tensor, bounds):
+            for key in [k for k, e in _layouts.items() if e.ref() is None]:
+                del _layouts[key]
+            entry = _RecordLayout(dag_tensor, bounds)
+            _layouts[id(dag_tensor)] = entry
+        return entry.scenes
+
+
 def cast_rays(
     dag_tensor: torch.Tensor,
     origins: torch.Tensor,
@@ -127,6 +176,8 @@ def cast_rays(
     *,
     hit_epsilon: float = HIT_EPSILON,
     out_steps: Any | None = None,
+    elevation_bins: int = 0,
+    kernel: str = "auto",
 ) -> None:
     """Batched bounded stackless sphere tracing (bindings.cpp:112-120 surface)."""
     validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics, max_steps,
@@ -139,8 +190,23 @@ def cast_rays(
     if not skip_direction_validation:
         _validate_direction_norms(dirs)
 
-    n_rays = int(origins.size(0)) * int(origins.size(1))
+    _check(kernel in ("auto", "raw"), f"kernel must be 'auto' or 'raw'; got {kernel!r}")
+    n_envs, rays = int(origins.size(0)), int(origins.size(1))
+    n_rays = n_envs * rays
     dev = dag_tensor.device
+    scenes = _record_layout(dag_tensor, bbox_min, bbox_max) if kernel == "auto" and n_rays <= (1 << 30) else None
+    if scenes is not None:
+        with torch.cuda.device(dev):
+            stream = torch.cuda.current_stream(dev).cuda_stream
+            code = _native.lib().navi_trace_relaid(
+                scenes.records.data_ptr(), scenes.n_records, scenes.relaid_table.data_ptr(), 1,
+                scenes.root_tables.data_ptr(), None, None, n_envs, rays, int(elevation_bins),
+                origins.data_ptr(), dirs.data_ptr(), out_distances.data_ptr(), out_semantics.data_ptr(),
+                int(max_steps), float(max_distance), float(hit_epsilon),
+                out_steps.data_ptr() if out_steps is not None else None, stream,
+            )
+        _native.check(code)
+        return
     with torch.cuda.device(dev):
         stream = torch.cuda.current_stream(dev).cuda_stream
         code = _native.lib().navi_cast_rays(

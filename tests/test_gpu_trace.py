@@ -29,7 +29,7 @@ def _cuda(x, dtype=None):
 
 
 def gpu_trace(words, origins, dirs, max_steps, max_distance, bmin, bmax, res=1, hit_epsilon=0.01,
-              skip=True, stream=None):
+              skip=True, stream=None, kernel="auto"):
     """Run the drop-in cast_rays; returns numpy (distance, semantic, steps)."""
     import torch
     from navi_amd import torch_sdf
@@ -46,22 +46,23 @@ def gpu_trace(words, origins, dirs, max_steps, max_distance, bmin, bmax, res=1, 
     out_n = torch.full(o.shape[:2], -7, device="cuda", dtype=torch.int32)
     if stream is None:
         torch_sdf.cast_rays(dag, to, td, out_d, out_s, max_steps, max_distance, list(bmin), list(bmax),
-                            res, skip, hit_epsilon=hit_epsilon, out_steps=out_n)
+                            res, skip, hit_epsilon=hit_epsilon, out_steps=out_n, kernel=kernel)
         torch.cuda.synchronize()
     else:
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
             torch_sdf.cast_rays(dag, to, td, out_d, out_s, max_steps, max_distance, list(bmin),
-                                list(bmax), res, skip, hit_epsilon=hit_epsilon, out_steps=out_n)
+                                list(bmax), res, skip, hit_epsilon=hit_epsilon, out_steps=out_n, kernel=kernel)
         stream.synchronize()
     return out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy()
 
 
 def assert_parity(words, origins, dirs, max_steps, max_distance, bmin, bmax, hit_epsilon=0.01,
-                  label=""):
+                  label="", kernel="auto"):
     o = np.asarray(origins, np.float32)
     d = np.asarray(dirs, np.float32)
-    gd, gs, gn = gpu_trace(words, o, d, max_steps, max_distance, bmin, bmax, hit_epsilon=hit_epsilon)
+    gd, gs, gn = gpu_trace(words, o, d, max_steps, max_distance, bmin, bmax, hit_epsilon=hit_epsilon,
+                           kernel=kernel)
     ref = oracle.trace(words, o.reshape(gd.shape + (3,)), d.reshape(gd.shape + (3,)), max_steps,
                        max_distance, bmin, bmax, hit_epsilon=hit_epsilon, threads=8)
     rd, rs, rn = ref["distance"], ref["semantic"], ref["steps"]
@@ -83,11 +84,12 @@ def _words(case):
     return np.array([int(w, 16) for w in case["words"]], dtype=np.uint64)
 
 
+@pytest.mark.parametrize("kernel", ["auto", "raw"])
 @pytest.mark.parametrize("case", json.loads(GOLDEN.read_text())["cases"], ids=lambda c: c["name"])
-def test_known_answers(gpu, case):
+def test_known_answers(gpu, case, kernel):
     gd, gs, gn = gpu_trace(_words(case), case["origins"], case["dirs"], case["max_steps"],
                            case["max_distance"], case["bbox_min"], case["bbox_max"], case["resolution"],
-                           skip=False)
+                           skip=False, kernel=kernel)
     for i, e in enumerate(case["expect"]):
         assert int(gs[0, i]) == e["semantic"], (case["name"], i)
         if "atol" in e:
@@ -96,7 +98,7 @@ def test_known_answers(gpu, case):
             assert float(gd[0, i]) > e["distance_gt"], (case["name"], i, gd[0, i])
     assert_parity(_words(case), np.array(case["origins"])[None], np.array(case["dirs"])[None],
                   case["max_steps"], case["max_distance"], case["bbox_min"], case["bbox_max"],
-                  label=case["name"])
+                  label=case["name"], kernel=kernel)
 
 
 def test_overwrites_preallocated_outputs_between_calls(gpu):
@@ -125,15 +127,16 @@ def room_scene():
     return scene
 
 
+@pytest.mark.parametrize("kernel", ["auto", "raw"])
 @pytest.mark.parametrize("hit_epsilon", [0.01, 1e-3])
-def test_room_scene_panorama_parity(gpu, room_scene, hit_epsilon):
+def test_room_scene_panorama_parity(gpu, room_scene, hit_epsilon, kernel):
     """Config-1 shape: 1 env x 64 az x 16 el from a free-space origin, 64 steps, 30 m."""
     rng = np.random.default_rng(1)
     origin = sf.free_origin(room_scene, rng)
     dirs = oracle.yaw_rotate(oracle.ray_directions(64, 16), rng.uniform(0, 2 * math.pi, 1))
     origins = np.broadcast_to(origin, dirs.shape).copy()
     stats = assert_parity(room_scene["words"], origins, dirs, 64, 30.0, room_scene["bmin"],
-                          room_scene["bmax"], hit_epsilon=hit_epsilon, label="room")
+                          room_scene["bmax"], hit_epsilon=hit_epsilon, label="room", kernel=kernel)
     assert stats["hits"] > 0
 
 
@@ -263,3 +266,39 @@ def test_empty_batches(gpu, shape):
     torch_sdf.cast_rays(dag, o, d, out_d, out_s, 4, 10.0, [0, 0, 0], [1, 1, 1], 1,
                         skip_direction_validation=True)
     torch.cuda.synchronize()
+
+
+def test_dropin_layout_cache_follows_the_tensor(gpu, room_scene):
+    """The record-layout copy behind kernel="auto" is rebuilt when the DAG tensor is
+    written in place, replaced, or traced with another bbox."""
+    import torch
+    from navi_amd import torch_sdf
+
+    rng = np.random.default_rng(5)
+    words = room_scene["words"].copy()
+    origin = sf.free_origin(room_scene, rng)
+    dirs = oracle.ray_directions(32, 8)[None]
+    origins = np.broadcast_to(origin, dirs.shape).copy()
+    dag = _cuda(words.view(np.int64))
+    o, d = _cuda(origins), _cuda(dirs)
+    out_d = torch.empty((1, dirs.shape[1]), device="cuda")
+    out_s = torch.empty((1, dirs.shape[1]), device="cuda", dtype=torch.int32)
+
+    def check(w, bmin, bmax):
+        torch_sdf.cast_rays(dag, o, d, out_d, out_s, 64, 30.0, bmin, bmax, 1, True)
+        torch.cuda.synchronize()
+        ref = oracle.trace(w, origins, dirs, 64, 30.0, bmin, bmax)
+        assert np.array_equal(out_d.cpu().numpy().view(np.uint32), ref["distance"].view(np.uint32))
+        assert np.array_equal(out_s.cpu().numpy(), ref["semantic"])
+
+    bmin, bmax = list(room_scene["bmin"]), list(room_scene["bmax"])
+    check(words, bmin, bmax)
+    check(words, bmin, bmax)  # cached
+    # every leaf of the DAG gets distance 0.25 and semantic 9: different results
+    leaf = (words >> np.uint64(63)) == 1
+    words[leaf] = np.uint64((1 << 63) | (9 << 16) | 0x3400)
+    dag.copy_(_cuda(words.view(np.int64)))  # in-place write bumps the version counter
+    check(words, bmin, bmax)
+    check(words, [v - 1.0 for v in bmin], [v + 1.0 for v in bmax])
+    dag = _cuda(room_scene["words"].view(np.int64))  # a new tensor
+    check(room_scene["words"], bmin, bmax)
