@@ -177,46 +177,71 @@ int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const n
                             int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                             void* stream);
 
+/* Point-SDF queries (device pointers; see navi_point_query). */
+typedef struct navi_point_queries {
+    const uint32_t* records;           /* the record pool of navi_trace_relaid */
+    uint64_t n_records;
+    const navi_relaid_scene* scenes;
+    int32_t n_scenes;
+    const uint64_t* root_tables;
+    const int32_t* point_scene;        /* [n_points] scene ids, or NULL: scene 0 */
+    const float* points;               /* [n_points][3] */
+    int64_t n_points;
+    float* out_distances;              /* [n_points] */
+    int32_t* out_semantics;            /* [n_points] */
+    int32_t* out_kind;                 /* [n_points] or NULL */
+} navi_point_queries;
+
 /*
  * Point-SDF queries (no reference kernel; the query of
  * projects/torch-sdf/cpp_src/kernel.cu:88-200 from the root, without caches)
- * over the device layout. Point i (3 floats) is looked up in scene
- * point_scene[i] (NULL: scene 0). Outputs per point: distance, semantic and,
- * if out_kind is non-NULL, the kind: 0 outside the scene box (1000, 0);
- * 1 leaf (its fp16 distance and semantic); 2 void cell (side along x times
- * 1.7321: the compiler prunes an octant only when every sample in it clears
- * its half-diagonal, projects/voxel-dag/src/compiler.cpp:626,639-643, so this
- * is a clearance lower bound; semantic 0); 3 the 32-level limit (NaN, 0);
- * 4 out-of-range data or an unknown scene id (NaN, 0).
+ * over the device layout. Point i is looked up in scene point_scene[i].
+ * Outputs per point: distance, semantic and, if out_kind is non-NULL, the
+ * kind: 0 outside the scene box (1000, 0); 1 leaf (its fp16 distance and
+ * semantic); 2 void cell (side along x times 1.7321: the compiler prunes an
+ * octant only when every sample in it clears its half-diagonal,
+ * projects/voxel-dag/src/compiler.cpp:626,639-643, so this is a clearance
+ * lower bound; semantic 0); 3 the 32-level limit (NaN, 0); 4 out-of-range
+ * data or an unknown scene id (NaN, 0).
  */
-int navi_point_query(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                     int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene,
-                     const float* points, int64_t n_points, float* out_distances, int32_t* out_semantics,
-                     int32_t* out_kind, void* stream);
+int navi_point_query(const navi_point_queries* queries, void* stream);
+
+/* The observation post-pass (device pointers; see navi_observe). */
+typedef struct navi_observation {
+    const float* distances;            /* [n_envs][Az * El], flat index az * El + el */
+    const int32_t* semantics;          /* [n_envs][Az * El]; needed for obs */
+    int64_t n_envs;
+    int32_t azimuth_bins, elevation_bins;
+    float max_distance;
+    float structure_band_min, structure_band_max;  /* reference defaults 1.5, 30 */
+    float proximity_threshold;                     /* 2 */
+    float collision_clearance;                     /* 0.15 */
+    void* depth_f16;                   /* [n_envs][1][El][Az] IEEE binary16, or NULL */
+    float* obs;                        /* [n_envs][3][Az][El]: depth, semantic, valid; or NULL */
+    float* prev_depth;                 /* [n_envs][Az][El]: read, then overwritten by depth */
+    float* delta;                      /* [n_envs][Az][El]: depth - prev_depth, or NULL */
+    float* stats;                      /* [n_envs][5], or NULL */
+    int32_t* collision;                /* [n_envs], or NULL */
+} navi_observation;
 
 /*
  * Observation post-pass in one launch (replaces the tensor code of
  * projects/environment/src/navi_environment/backends/sdfdag_backend.py:
- * 366-473 and the collision test of :1340), optionally fused with point
- * queries (as navi_point_query; n_points 0 for none). distances is
- * n_envs x (azimuth_bins * elevation_bins) floats, flat index az * El + el.
- * Per env: clamped c = clamp(d, 0, max_distance) (NaN stays NaN);
- * out_depth_f16 (optional, IEEE binary16, n_envs x El x Az: transposed)
- * = clamp(log1p(c) / log1p(max_distance), 0, 1); out_stats (optional,
- * n_envs x 5 floats) = min c (NaN if any is NaN), starvation ratio
- * (c >= max_distance - 1e-3), proximity ratio (finite and
- * c <= proximity_threshold; 0 if the threshold is <= 0), structure-band ratio
- * (finite and band_min <= c <= band_max; 0 unless band_max > band_min) and
- * forward structure ratio (the same over the first and last max(1, Az / 6)
- * azimuth bins); out_collision (optional, n_envs int32) = min c <
- * collision_clearance.
+ * 366-473, the collision test of :1340 and the observation stack and delta
+ * of :1501-1526), optionally fused with point queries (as navi_point_query;
+ * queries may be NULL, observation may be NULL for queries alone). Per env:
+ * c = clamp(d, 0, max_distance) (NaN stays NaN); depth = clamp(log1p(c) /
+ * log1p(max_distance), 0, 1); depth_f16 = depth transposed to (El, Az); obs =
+ * (depth, float(semantic), float(isfinite(d))) in (Az, El) order; delta =
+ * depth - prev_depth, or 0 for an env whose prev_depth sums below 1e-6 in
+ * absolute value, after which prev_depth holds depth; stats = min c (NaN if
+ * any is NaN), starvation ratio (c >= max_distance - 1e-3), proximity ratio
+ * (finite and c <= proximity_threshold; 0 if that is <= 0), structure-band
+ * ratio (finite and band_min <= c <= band_max; 0 unless band_max > band_min)
+ * and forward structure ratio (the same over the first and last
+ * max(1, Az / 6) azimuth bins); collision = min c < collision_clearance.
  */
-int navi_observe(const float* distances, int64_t n_envs, int32_t azimuth_bins, int32_t elevation_bins,
-                 float max_distance, float structure_band_min, float structure_band_max, float proximity_threshold,
-                 float collision_clearance, void* out_depth_f16, float* out_stats, int32_t* out_collision,
-                 const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes, int32_t n_scenes,
-                 const uint64_t* root_tables, const int32_t* point_scene, const float* points, int64_t n_points,
-                 float* point_distances, int32_t* point_semantics, int32_t* point_kind, void* stream);
+int navi_observe(const navi_observation* observation, const navi_point_queries* queries, void* stream);
 
 /* Message of the last failure on the calling thread ("" if none). The
  * reference surfaces failures as c10::Error via TORCH_CHECK (bindings.cpp:57-89). */

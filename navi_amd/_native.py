@@ -66,15 +66,31 @@ _lib.navi_trace_relaid_poses.argtypes = [
     _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp,
     _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
+
+
+class PointQueries(ctypes.Structure):
+    """navi_point_queries (include/navi_trace.h)."""
+
+    _fields_ = [("records", _vp), ("n_records", ctypes.c_uint64), ("scenes", _vp), ("n_scenes", ctypes.c_int32),
+                ("root_tables", _vp), ("point_scene", _vp), ("points", _vp), ("n_points", ctypes.c_int64),
+                ("out_distances", _vp), ("out_semantics", _vp), ("out_kind", _vp)]
+
+
+class Observation(ctypes.Structure):
+    """navi_observation (include/navi_trace.h)."""
+
+    _fields_ = [("distances", _vp), ("semantics", _vp), ("n_envs", ctypes.c_int64),
+                ("azimuth_bins", ctypes.c_int32), ("elevation_bins", ctypes.c_int32),
+                ("max_distance", ctypes.c_float), ("structure_band_min", ctypes.c_float),
+                ("structure_band_max", ctypes.c_float), ("proximity_threshold", ctypes.c_float),
+                ("collision_clearance", ctypes.c_float), ("depth_f16", _vp), ("obs", _vp), ("prev_depth", _vp),
+                ("delta", _vp), ("stats", _vp), ("collision", _vp)]
+
+
 _lib.navi_point_query.restype = ctypes.c_int
-_lib.navi_point_query.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, _vp, _vp,
-                                  _vp, _vp]
+_lib.navi_point_query.argtypes = [ctypes.POINTER(PointQueries), _vp]
 _lib.navi_observe.restype = ctypes.c_int
-_lib.navi_observe.argtypes = [
-    _vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_float, ctypes.c_float, ctypes.c_float,
-    ctypes.c_float, ctypes.c_float, _vp, _vp, _vp, _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp,
-    ctypes.c_int64, _vp, _vp, _vp, _vp,
-]
+_lib.navi_observe.argtypes = [ctypes.POINTER(Observation), ctypes.POINTER(PointQueries), _vp]
 
 # Layout of navi_relaid_scene (include/navi_trace.h), 48 bytes.
 RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot", "<u4"),

@@ -35,16 +35,13 @@ constexpr float kVoidClearance = 1.7321f;  // compiler.cpp:626,639-643: pruned o
 enum : int32_t { kKindOutside = 0, kKindLeaf = 1, kKindVoid = 2, kKindDepth = 3, kKindFault = 4 };
 
 struct PostParams {
-    const float* __restrict__ dist;  // [n_envs][az * el]
-    int32_t n_envs, az, el;
-    float max_distance, band_min, band_max, proximity, clearance;
+    navi_observation O;  // the post-pass (see include/navi_trace.h)
+    int32_t n_envs;
     // The reference compares float32 tensors with Python floats and divides
     // by one: the host rounds max_distance - 1e-3 and log1p(max_distance),
     // evaluated in double, to float, as torch does with such scalars.
     float saturation, log_denom;
-    _Float16* __restrict__ depth16;  // [n_envs][el][az] or null
-    float* __restrict__ stats;       // [n_envs][5] or null
-    int32_t* __restrict__ collision;  // [n_envs] or null
+    int32_t stage16;  // stage the transposed fp16 tile in LDS (n halves fit)
     // point queries
     const uint32_t* __restrict__ records;
     uint32_t n_records;
@@ -157,34 +154,68 @@ __global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
         if (i < P.n_points) point_query(P, i);
         return;
     }
+    extern __shared__ _Float16 lds16[];  // the env's (El, Az) fp16 tile when staged
     __shared__ uint32_t lds_u[kThreads / 64];
     __shared__ float lds_f[kThreads / 64];
+    const navi_observation& O = P.O;
     const int32_t e = blockIdx.x;
-    const int32_t n = P.az * P.el;
-    const float* dist = P.dist + static_cast<int64_t>(e) * n;
+    const int32_t az = O.azimuth_bins, el = O.elevation_bins;
+    const int32_t n = az * el;
+    const int64_t base = static_cast<int64_t>(e) * n;
+    const float* dist = O.distances + base;
+    // sdfdag_backend.py:1510-1514: the delta is zero while the previous depth
+    // sums (in absolute value) below 1e-6, i.e. before the first frame
+    bool first = false;
+    if (O.delta) {
+        float acc = 0.0f;
+        for (int32_t k = threadIdx.x; k < n; k += kThreads) acc += fabsf(O.prev_depth[base + k]);
+        first = block_sum(acc, lds_f) < 1e-6f;
+    }
     // sdfdag_backend.py:390: the first and last Az/6 azimuth bins (at least one)
-    const int32_t fwd = max(1, P.az / 6);
-    const bool band = P.band_max > P.band_min;
+    const int32_t fwd = max(1, az / 6);
+    const bool band = O.structure_band_max > O.structure_band_min;
     uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0;
     float mn = INFINITY;
     for (int32_t k = threadIdx.x; k < n; k += kThreads) {
         const float m = dist[k];
         const bool valid = isfinite(m);
         // torch.clamp(min=0, max=max_distance): NaN stays NaN
-        const float c = (m != m) ? m : fminf(fmaxf(m, 0.0f), P.max_distance);
+        const float c = (m != m) ? m : fminf(fmaxf(m, 0.0f), O.max_distance);
         mn = nan_min(mn, c);
         n_sat += (c >= P.saturation) ? 1u : 0u;
-        n_prox += (valid && c <= P.proximity) ? 1u : 0u;
-        const bool in_band = band && valid && c >= P.band_min && c <= P.band_max;
+        n_prox += (valid && c <= O.proximity_threshold) ? 1u : 0u;
+        const bool in_band = band && valid && c >= O.structure_band_min && c <= O.structure_band_max;
         n_band += in_band ? 1u : 0u;
-        const int32_t a = k / P.el;
+        const int32_t a = k / el;
         // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
-        n_fwd += in_band ? static_cast<uint32_t>((a < fwd ? 1 : 0) + (a >= P.az - fwd ? 1 : 0)) : 0u;
-        if (P.depth16) {
-            const float q = c != c ? c : fminf(fmaxf(log1pf(c) / P.log_denom, 0.0f), 1.0f);
-            P.depth16[static_cast<int64_t>(e) * n + static_cast<int64_t>(k % P.el) * P.az + a] =
-                static_cast<_Float16>(q);
+        n_fwd += in_band ? static_cast<uint32_t>((a < fwd ? 1 : 0) + (a >= az - fwd ? 1 : 0)) : 0u;
+        // sdfdag_backend.py:441-443
+        const float q = c != c ? c : fminf(fmaxf(log1pf(c) / P.log_denom, 0.0f), 1.0f);
+        if (O.obs) {  // sdfdag_backend.py:1516-1524: stack(depth, semantic, valid), (Az, El) order
+            float* ob = O.obs + 3 * base;
+            ob[k] = q;
+            ob[n + k] = static_cast<float>(O.semantics[base + k]);
+            ob[2 * n + k] = valid ? 1.0f : 0.0f;
         }
+        if (O.delta) {  // sdfdag_backend.py:1509-1515
+            const float pv = O.prev_depth[base + k];
+            O.delta[base + k] = first ? 0.0f : q - pv;
+            O.prev_depth[base + k] = q;
+        }
+        if (O.depth_f16) {
+            const int32_t t = (k - a * el) * az + a;  // transposed: (El, Az)
+            if (P.stage16) {
+                lds16[t] = static_cast<_Float16>(q);
+            } else {
+                static_cast<_Float16*>(O.depth_f16)[base + t] = static_cast<_Float16>(q);
+            }
+        }
+    }
+    if (O.depth_f16 && P.stage16) {
+        __syncthreads();
+        uint32_t* out = reinterpret_cast<uint32_t*>(static_cast<_Float16*>(O.depth_f16) + base);
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(lds16);
+        for (int32_t k = threadIdx.x; k < n / 2; k += kThreads) out[k] = src[k];
     }
     n_sat = block_sum(n_sat, lds_u);
     n_prox = block_sum(n_prox, lds_u);
@@ -193,15 +224,15 @@ __global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
     mn = block_min(mn, lds_f);
     if (threadIdx.x == 0) {
         const float fn = static_cast<float>(n);
-        if (P.stats) {
-            float* st = P.stats + 5 * static_cast<int64_t>(e);
+        if (O.stats) {
+            float* st = O.stats + 5 * static_cast<int64_t>(e);
             st[0] = mn;
             st[1] = static_cast<float>(n_sat) / fn;
-            st[2] = P.proximity > 0.0f ? static_cast<float>(n_prox) / fn : 0.0f;
+            st[2] = O.proximity_threshold > 0.0f ? static_cast<float>(n_prox) / fn : 0.0f;
             st[3] = band ? static_cast<float>(n_band) / fn : 0.0f;
-            st[4] = band ? static_cast<float>(n_fwd) / static_cast<float>(2 * fwd * P.el) : 0.0f;
+            st[4] = band ? static_cast<float>(n_fwd) / static_cast<float>(2 * fwd * el) : 0.0f;
         }
-        if (P.collision) P.collision[e] = mn < P.clearance ? 1 : 0;  // sdfdag_backend.py:1340
+        if (O.collision) O.collision[e] = mn < O.collision_clearance ? 1 : 0;  // sdfdag_backend.py:1340
     }
 }
 
@@ -209,84 +240,70 @@ int launch(const PostParams& P, hipStream_t stream) {
     const int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
     const int64_t blocks = static_cast<int64_t>(P.env_blocks) + point_blocks;
     if (blocks == 0) return NAVI_OK;
-    hipLaunchKernelGGL(observation_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream, P);
+    const size_t lds = P.stage16 ? static_cast<size_t>(P.O.azimuth_bins) * P.O.elevation_bins * 2 : 0;
+    hipLaunchKernelGGL(observation_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;
 }
 
-int points_setup(PostParams& P, const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                 int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene, const float* points,
-                 int64_t n_points, float* out_d, int32_t* out_s, int32_t* out_kind) {
-    if (n_points < 0 || n_points > (1LL << 30)) return set_error(NAVI_E_ARG, "n_points must be in [0, 2^30]");
-    if (n_points == 0) return NAVI_OK;
-    if (!points || !out_d || !out_s) return set_error(NAVI_E_ARG, "points and point outputs must be non-null");
-    if (n_scenes <= 0 || !scenes || !records || !root_tables)
+int points_setup(PostParams& P, const navi_point_queries* Q) {
+    if (Q == nullptr || Q->n_points == 0) return NAVI_OK;
+    if (Q->n_points < 0 || Q->n_points > (1LL << 30)) return set_error(NAVI_E_ARG, "n_points must be in [0, 2^30]");
+    if (!Q->points || !Q->out_distances || !Q->out_semantics)
+        return set_error(NAVI_E_ARG, "points and point outputs must be non-null");
+    if (Q->n_scenes <= 0 || !Q->scenes || !Q->records || !Q->root_tables)
         return set_error(NAVI_E_ARG, "scene table, records and root_tables must be non-empty");
-    if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
-    P.records = records;
-    P.n_records = static_cast<uint32_t>(n_records);
-    P.scenes = scenes;
-    P.n_scenes = n_scenes;
-    P.root_table = root_tables;
-    P.point_scene = point_scene;
-    P.points = points;
-    P.n_points = static_cast<int32_t>(n_points);
-    P.point_d = out_d;
-    P.point_s = out_s;
-    P.point_kind = out_kind;
+    if (Q->n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
+    P.records = Q->records;
+    P.n_records = static_cast<uint32_t>(Q->n_records);
+    P.scenes = Q->scenes;
+    P.n_scenes = Q->n_scenes;
+    P.root_table = Q->root_tables;
+    P.point_scene = Q->point_scene;
+    P.points = Q->points;
+    P.n_points = static_cast<int32_t>(Q->n_points);
+    P.point_d = Q->out_distances;
+    P.point_s = Q->out_semantics;
+    P.point_kind = Q->out_kind;
     return NAVI_OK;
 }
 
 }  // namespace
 }  // namespace navi
 
-extern "C" int navi_point_query(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                                int32_t n_scenes, const uint64_t* root_tables, const int32_t* point_scene,
-                                const float* points, int64_t n_points, float* out_distances,
-                                int32_t* out_semantics, int32_t* out_kind, void* stream) {
+extern "C" int navi_point_query(const navi_point_queries* queries, void* stream) {
     using namespace navi;
     PostParams P{};
-    const int code = points_setup(P, records, n_records, scenes, n_scenes, root_tables, point_scene, points, n_points,
-                                  out_distances, out_semantics, out_kind);
-    if (code != NAVI_OK || n_points == 0) return code;
+    const int code = points_setup(P, queries);
+    if (code != NAVI_OK || P.n_points == 0) return code;
     return launch(P, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int navi_observe(const float* distances, int64_t n_envs, int32_t azimuth_bins, int32_t elevation_bins,
-                            float max_distance, float structure_band_min, float structure_band_max,
-                            float proximity_threshold, float collision_clearance, void* out_depth_f16,
-                            float* out_stats, int32_t* out_collision, const uint32_t* records,
-                            uint64_t n_records, const navi_relaid_scene* scenes, int32_t n_scenes,
-                            const uint64_t* root_tables, const int32_t* point_scene, const float* points,
-                            int64_t n_points, float* point_distances, int32_t* point_semantics,
-                            int32_t* point_kind, void* stream) {
+extern "C" int navi_observe(const navi_observation* observation, const navi_point_queries* queries, void* stream) {
     using namespace navi;
-    if (n_envs < 0 || n_envs > 0x7fffffffLL) return set_error(NAVI_E_ARG, "n_envs must be in [0, 2^31)");
-    if (azimuth_bins <= 0 || elevation_bins <= 0 ||
-        static_cast<int64_t>(azimuth_bins) * elevation_bins > 0x7fffffffLL)
-        return set_error(NAVI_E_ARG, "azimuth_bins and elevation_bins must be positive");
-    if (!std::isfinite(max_distance) || !(max_distance > 0.0f))
-        return set_error(NAVI_E_ARG, "max_distance must be a finite positive float");
-    if (n_envs > 0 && !distances) return set_error(NAVI_E_ARG, "distances must be non-null");
     PostParams P{};
-    P.dist = distances;
-    P.n_envs = static_cast<int32_t>(n_envs);
-    P.az = azimuth_bins;
-    P.el = elevation_bins;
-    P.max_distance = max_distance;
-    P.saturation = static_cast<float>(static_cast<double>(max_distance) - 1e-3);
-    P.log_denom = static_cast<float>(std::log1p(static_cast<double>(max_distance)));
-    P.band_min = structure_band_min;
-    P.band_max = structure_band_max;
-    P.proximity = proximity_threshold;
-    P.clearance = collision_clearance;
-    P.depth16 = static_cast<_Float16*>(out_depth_f16);
-    P.stats = out_stats;
-    P.collision = out_collision;
-    P.env_blocks = static_cast<int32_t>(n_envs);
-    const int code = points_setup(P, records, n_records, scenes, n_scenes, root_tables, point_scene, points, n_points,
-                                  point_distances, point_semantics, point_kind);
+    if (observation != nullptr && observation->n_envs > 0) {
+        const navi_observation& O = *observation;
+        if (O.n_envs > 0x7fffffffLL) return set_error(NAVI_E_ARG, "n_envs must be below 2^31");
+        if (O.azimuth_bins <= 0 || O.elevation_bins <= 0 ||
+            static_cast<int64_t>(O.azimuth_bins) * O.elevation_bins > (1LL << 26))
+            return set_error(NAVI_E_ARG, "azimuth_bins and elevation_bins must be positive, product <= 2^26");
+        if (!std::isfinite(O.max_distance) || !(O.max_distance > 0.0f))
+            return set_error(NAVI_E_ARG, "max_distance must be a finite positive float");
+        if (!O.distances) return set_error(NAVI_E_ARG, "distances must be non-null");
+        if (O.obs && !O.semantics) return set_error(NAVI_E_ARG, "obs needs semantics");
+        if (O.delta && !O.prev_depth) return set_error(NAVI_E_ARG, "delta needs prev_depth");
+        P.O = O;
+        P.n_envs = static_cast<int32_t>(O.n_envs);
+        P.env_blocks = P.n_envs;
+        P.saturation = static_cast<float>(static_cast<double>(O.max_distance) - 1e-3);
+        P.log_denom = static_cast<float>(std::log1p(static_cast<double>(O.max_distance)));
+        const int64_t n = static_cast<int64_t>(O.azimuth_bins) * O.elevation_bins;
+        // a 48 KiB tile at most, and an even count for the 4-byte copy out
+        P.stage16 = (O.depth_f16 != nullptr && n % 2 == 0 && n * 2 <= 48 * 1024) ? 1 : 0;
+    }
+    const int code = points_setup(P, queries);
     if (code != NAVI_OK) return code;
     return launch(P, static_cast<hipStream_t>(stream));
 }

@@ -10,6 +10,7 @@ per env selects the DAG inside the kernel.
 
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Any, Sequence
 
@@ -211,61 +212,66 @@ class ResidentScenes:
                 float(max_distance), float(hit_epsilon), ptrs[6], stream)
         _native.check(code)
 
+    def _point_queries(self, points, out_distances, out_semantics, point_scene, out_kind, prefix=""):
+        self._require_relaid()
+        p = int(points.shape[0])
+        q = _native.PointQueries()
+        q.records, q.n_records = self.records.data_ptr(), self.n_records
+        q.scenes, q.n_scenes, q.root_tables = self.relaid_table.data_ptr(), self.n_scenes, self.root_tables.data_ptr()
+        q.points = self._check("points", points, torch.float32, (p, 3))
+        q.n_points = p
+        q.point_scene = self._check(prefix + "point_scene", point_scene, torch.int32, (p,), optional=True)
+        q.out_distances = self._check(prefix + "distances", out_distances, torch.float32, (p,))
+        q.out_semantics = self._check(prefix + "semantics", out_semantics, torch.int32, (p,))
+        q.out_kind = self._check(prefix + "kind", out_kind, torch.int32, (p,), optional=True)
+        return q
+
     def point_query(self, points: torch.Tensor, out_distances: torch.Tensor, out_semantics: torch.Tensor, *,
                     point_scene: torch.Tensor | None = None, out_kind: torch.Tensor | None = None) -> None:
         """Point-SDF queries ``points [P, 3]`` (scene ``point_scene[i]``, default 0); see
         ``navi_point_query`` in ``include/navi_trace.h`` for the result kinds."""
-        self._require_relaid()
-        p = int(points.shape[0])
-        ptrs = [self._check("points", points, torch.float32, (p, 3)),
-                self._check("out_distances", out_distances, torch.float32, (p,)),
-                self._check("out_semantics", out_semantics, torch.int32, (p,)),
-                self._check("point_scene", point_scene, torch.int32, (p,), optional=True),
-                self._check("out_kind", out_kind, torch.int32, (p,), optional=True)]
+        q = self._point_queries(points, out_distances, out_semantics, point_scene, out_kind)
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            code = _native.lib().navi_point_query(
-                self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                self.root_tables.data_ptr(), ptrs[3], ptrs[0], p, ptrs[1], ptrs[2], ptrs[4], stream)
+            code = _native.lib().navi_point_query(ctypes.byref(q), stream)
         _native.check(code)
 
     def observe(self, distances: torch.Tensor, azimuth_bins: int, elevation_bins: int, max_distance: float, *,
                 structure_band_min: float = 1.5, structure_band_max: float = 30.0,
                 proximity_threshold: float = 2.0, collision_clearance: float = 0.15,
                 out_depth_f16: torch.Tensor | None = None, out_stats: torch.Tensor | None = None,
-                out_collision: torch.Tensor | None = None, points: torch.Tensor | None = None,
+                out_collision: torch.Tensor | None = None, semantics: torch.Tensor | None = None,
+                out_obs: torch.Tensor | None = None, prev_depth: torch.Tensor | None = None,
+                out_delta: torch.Tensor | None = None, points: torch.Tensor | None = None,
                 point_scene: torch.Tensor | None = None, point_distances: torch.Tensor | None = None,
                 point_semantics: torch.Tensor | None = None, point_kind: torch.Tensor | None = None) -> None:
-        """The observation post-pass of ``sdfdag_backend.py:366-473,1340`` in one launch, with
-        optional point queries fused in. ``distances [E, Az*El]``; writes ``out_depth_f16
-        [E, 1, El, Az]`` (float16), ``out_stats [E, 5]`` (min distance, starvation, proximity,
-        structure-band and forward-structure ratios), ``out_collision [E]`` (int32). Defaults
-        are the reference's (``sdfdag_backend.py:38,48-51``)."""
+        """The observation post-pass of ``sdfdag_backend.py:366-473,1340,1501-1526`` in one
+        launch, with optional point queries fused in. ``distances [E, Az*El]``; writes any of
+        ``out_depth_f16 [E, 1, El, Az]`` (float16), ``out_obs [E, 3, Az, El]`` (depth,
+        semantic, valid; needs ``semantics [E, Az*El]``), ``out_delta [E, Az, El]`` (against
+        ``prev_depth``, which then holds the depth), ``out_stats [E, 5]`` (min distance,
+        starvation, proximity, structure-band and forward-structure ratios) and
+        ``out_collision [E]`` (int32). Defaults are the reference's
+        (``sdfdag_backend.py:38,48-51``)."""
         e = int(distances.shape[0])
-        n = int(azimuth_bins) * int(elevation_bins)
-        d_ptr = self._check("distances", distances, torch.float32, (e, n))
-        outs = [self._check("out_depth_f16", out_depth_f16, torch.float16,
-                            (e, 1, int(elevation_bins), int(azimuth_bins)), optional=True),
-                self._check("out_stats", out_stats, torch.float32, (e, 5), optional=True),
-                self._check("out_collision", out_collision, torch.int32, (e,), optional=True)]
-        n_pts = 0
-        pp = [None] * 5
+        az, el = int(azimuth_bins), int(elevation_bins)
+        o = _native.Observation()
+        o.distances = self._check("distances", distances, torch.float32, (e, az * el))
+        o.semantics = self._check("semantics", semantics, torch.int32, (e, az * el), optional=out_obs is None)
+        o.n_envs, o.azimuth_bins, o.elevation_bins = e, az, el
+        o.max_distance = float(max_distance)
+        o.structure_band_min, o.structure_band_max = float(structure_band_min), float(structure_band_max)
+        o.proximity_threshold, o.collision_clearance = float(proximity_threshold), float(collision_clearance)
+        o.depth_f16 = self._check("out_depth_f16", out_depth_f16, torch.float16, (e, 1, el, az), optional=True)
+        o.obs = self._check("out_obs", out_obs, torch.float32, (e, 3, az, el), optional=True)
+        o.prev_depth = self._check("prev_depth", prev_depth, torch.float32, (e, az, el), optional=out_delta is None)
+        o.delta = self._check("out_delta", out_delta, torch.float32, (e, az, el), optional=True)
+        o.stats = self._check("out_stats", out_stats, torch.float32, (e, 5), optional=True)
+        o.collision = self._check("out_collision", out_collision, torch.int32, (e,), optional=True)
+        q = None
         if points is not None:
-            self._require_relaid()
-            n_pts = int(points.shape[0])
-            pp = [self._check("points", points, torch.float32, (n_pts, 3)),
-                  self._check("point_scene", point_scene, torch.int32, (n_pts,), optional=True),
-                  self._check("point_distances", point_distances, torch.float32, (n_pts,)),
-                  self._check("point_semantics", point_semantics, torch.int32, (n_pts,)),
-                  self._check("point_kind", point_kind, torch.int32, (n_pts,), optional=True)]
-        rec = self.records.data_ptr() if self.relaid_ok else None
+            q = self._point_queries(points, point_distances, point_semantics, point_scene, point_kind, "point_")
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
-            code = _native.lib().navi_observe(
-                d_ptr, e, int(azimuth_bins), int(elevation_bins), float(max_distance), float(structure_band_min),
-                float(structure_band_max), float(proximity_threshold), float(collision_clearance), outs[0],
-                outs[1], outs[2], rec, self.n_records if self.relaid_ok else 0,
-                self.relaid_table.data_ptr() if self.relaid_ok else None, self.n_scenes,
-                self.root_tables.data_ptr() if self.relaid_ok else None, pp[1], pp[0], n_pts, pp[2], pp[3],
-                pp[4], stream)
+            code = _native.lib().navi_observe(ctypes.byref(o), ctypes.byref(q) if q is not None else None, stream)
         _native.check(code)

@@ -349,21 +349,38 @@ def observation_ratios(clamped, valid, max_distance: float, band_min: float, ban
 
 
 def observe(out_distances, az_bins: int, el_bins: int, max_distance: float, band_min: float = 1.5,
-            band_max: float = 30.0, proximity: float = 2.0, clearance: float = 0.15) -> dict[str, np.ndarray]:
+            band_max: float = 30.0, proximity: float = 2.0, clearance: float = 0.15, semantics=None,
+            prev_depth=None) -> dict[str, np.ndarray]:
     """The observation step after a trace: ``depth16 (B, 1, El, Az)`` float16 (north-star
     layout of ``postprocess``'s depth), ``stats [B, 5]`` = min clamped distance and the four
-    ``observation_ratios``, ``collision [B]`` = min < clearance (sdfdag_backend.py:1340)."""
+    ``observation_ratios``, ``collision [B]`` = min < clearance (sdfdag_backend.py:1340); with
+    ``semantics``, ``obs (B, 3, Az, El)`` = stack(depth, semantic, valid) float32, and with
+    ``prev_depth (B, Az, El)``, ``delta`` = depth - prev_depth, zero for envs whose
+    prev_depth sums below 1e-6 in absolute value (``_consume_observation_batch``,
+    sdfdag_backend.py:1501-1526)."""
+    import torch
+
     d = np.asarray(out_distances, dtype=np.float32)
-    depth, _, valid, min_d, clamped = postprocess(d, np.zeros(d.shape, np.int32), az_bins, el_bins, max_distance)
+    sem = np.zeros(d.shape, np.int32) if semantics is None else np.asarray(semantics, np.int32)
+    depth, sem_t, valid, min_d, clamped = postprocess(d, sem, az_bins, el_bins, max_distance)
     ratios = observation_ratios(clamped.numpy(), valid.numpy(), max_distance, band_min, band_max, proximity)
     stats = np.concatenate([min_d.numpy()[:, None].astype(np.float32), ratios], axis=1)
     with np.errstate(invalid="ignore"):
         collision = (stats[:, 0] < np.float32(clearance)).astype(np.int32)
-    return {
+    out = {
         "depth16": depth.permute(0, 2, 1).unsqueeze(1).contiguous().numpy().astype(np.float16),
+        "depth": depth.numpy(),
         "stats": stats,
         "collision": collision,
     }
+    if semantics is not None:
+        out["obs"] = torch.stack((depth, sem_t.to(torch.float32), valid.to(torch.float32)), dim=1).numpy()
+    if prev_depth is not None:
+        prev = torch.as_tensor(np.asarray(prev_depth, np.float32))
+        first = prev.abs().sum(dim=(1, 2)) < 1e-6
+        delta = depth - prev
+        out["delta"] = torch.where(first.view(-1, 1, 1), torch.zeros_like(delta), delta).numpy()
+    return out
 
 
 if os.environ.get("NAVI_ORACLE_EAGER"):

@@ -139,3 +139,23 @@ def test_observation_ratios_by_hand():
     one = oracle.observe(np.array([[2.0, 20.0]], np.float32), 1, 2, 30.0, band_min=1.5, band_max=8.0)
     assert float(one["stats"][0, 4]) == 0.5
     assert one["depth16"].shape == (1, 1, 2, 1)
+
+
+def test_observation_stack_and_delta():
+    """_consume_observation_batch (sdfdag_backend.py:1501-1526) with the known values of
+    test_postprocessing_oracle.py::TestDeltaDepthComputation: delta = current - previous,
+    zero on the first frame (previous all zero); obs stacks depth, semantic, valid."""
+    az, el = 2, 2
+    d = np.array([[0.5, 1.0, np.inf, 3.0], [2.0, 2.0, 2.0, 2.0]], np.float32)
+    s = np.array([[1, 2, 0, 4], [5, 5, 5, 5]], np.int32)
+    prev = np.zeros((2, az, el), np.float32)
+    prev[0] = [[0.2, 0.3], [0.4, 0.5]]
+    out = oracle.observe(d, az, el, 10.0, semantics=s, prev_depth=prev)
+    ld = math.log1p(10.0)
+    want0 = np.array([[math.log1p(0.5), math.log1p(1.0)], [ld, math.log1p(3.0)]]) / ld
+    np.testing.assert_allclose(out["depth"][0], want0, atol=1e-6)
+    np.testing.assert_allclose(out["delta"][0], want0 - prev[0], atol=1e-6)
+    assert (out["delta"][1] == 0).all()  # previous frame was all zeros
+    assert out["obs"].shape == (2, 3, az, el)
+    assert out["obs"][0, 1].tolist() == [[1.0, 2.0], [0.0, 4.0]]
+    assert out["obs"][0, 2].tolist() == [[1.0, 1.0], [0.0, 1.0]]

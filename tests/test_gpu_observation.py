@@ -164,8 +164,11 @@ def _observe_oracle_check(got, want):
     assert (np.abs(np.nan_to_num(a) - np.nan_to_num(b)) <= ulp).all()
 
 
-@pytest.mark.parametrize("az,el,band", [(256, 48, (1.5, 30.0)), (12, 3, (1.5, 8.0)), (7, 5, (3.0, 3.0))])
+@pytest.mark.parametrize("az,el,band", [(256, 48, (1.5, 30.0)), (12, 3, (1.5, 8.0)), (7, 5, (3.0, 3.0)),
+                                         (256, 128, (1.5, 30.0))])
 def test_observe_matches_oracle(gpu, corpus, az, el, band):
+    """(256, 48) and (12, 3) stage the fp16 tile in LDS; (7, 5) (odd count) and
+    (256, 128) (64 KiB tile) write it directly."""
     import torch
 
     res = _resident(corpus)
@@ -175,16 +178,35 @@ def test_observe_matches_oracle(gpu, corpus, az, el, band):
     d[0, :5] = [np.inf, -np.inf, 0.0, 30.0, 29.999]
     d[1, 7] = np.nan
     d[2] = rng.uniform(0.0, 0.3, az * el)  # a collision
-    want = oracle.observe(d, az, el, 30.0, band[0], band[1], 2.0, 0.15)
+    sem = rng.integers(0, 40, (e, az * el)).astype(np.int32)
+    prev = rng.uniform(0.0, 1.0, (e, az, el)).astype(np.float32)
+    prev[3] = 0.0  # first frame for env 3
+    want = oracle.observe(d, az, el, 30.0, band[0], band[1], 2.0, 0.15, semantics=sem, prev_depth=prev)
     dev = res.device
     td = torch.from_numpy(d).to(dev)
+    ts = torch.from_numpy(sem).to(dev)
+    tprev = torch.from_numpy(prev).to(dev)
     d16 = torch.empty((e, 1, el, az), dtype=torch.float16, device=dev)
     st = torch.empty((e, 5), device=dev)
     co = torch.empty((e,), dtype=torch.int32, device=dev)
+    obs = torch.empty((e, 3, az, el), device=dev)
+    delta = torch.empty((e, az, el), device=dev)
     res.observe(td, az, el, 30.0, structure_band_min=band[0], structure_band_max=band[1], out_depth_f16=d16,
-                out_stats=st, out_collision=co)
+                out_stats=st, out_collision=co, semantics=ts, out_obs=obs, prev_depth=tprev, out_delta=delta)
     torch.cuda.synchronize()
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
+    # float32 outputs: depth within 2 ulp (log1pf versus torch CPU), semantic / valid exact
+    go = obs.cpu().numpy()
+    np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
+    wd = want["obs"][:, 0]
+    assert np.array_equal(np.isnan(go[:, 0]), np.isnan(wd))
+    np.testing.assert_allclose(np.nan_to_num(go[:, 0]), np.nan_to_num(wd), rtol=2.5e-7, atol=1e-7)
+    gdel = delta.cpu().numpy()
+    assert (gdel[3] == 0).all()
+    assert np.array_equal(np.isnan(gdel), np.isnan(want["delta"]))
+    np.testing.assert_allclose(np.nan_to_num(gdel), np.nan_to_num(want["delta"]), rtol=0, atol=3e-7)
+    # prev_depth now holds the depth
+    assert np.array_equal(tprev.cpu().numpy().view(np.uint32), go[:, 0].view(np.uint32))
 
 
 def test_observation_step_end_to_end(gpu, corpus):
