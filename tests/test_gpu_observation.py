@@ -246,3 +246,52 @@ def test_observation_step_end_to_end(gpu, corpus):
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
     assert np.array_equal(pk.cpu().numpy(), pwant[2]) and np.array_equal(ps.cpu().numpy(), pwant[1])
     assert _same_bits(pd.cpu().numpy(), pwant[0])
+
+
+def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
+    """The bench-sdfdag harness on a .gmdag file: the command runs and reports the
+    reference's summary keys, and one harness step's observation, delta and
+    statistics match the oracle pipeline on the rays that step cast."""
+    import json as _json
+
+    import torch
+
+    from navi_amd import bench_sdfdag, gmdag
+    from navi_amd import scenes as S
+
+    scene = S.box_room(seed=4, resolution=64)
+    path = tmp_path / "room.gmdag"
+    gmdag.write_gmdag(path, scene.compile(), scene.resolution, scene.bbox_min_list, scene.voxel_size)
+    assert bench_sdfdag.main(["--gmdag-file", str(path), "--actors", "6", "--steps", "3", "--warmup-steps", "1",
+                              "--azimuth-bins", "32", "--elevation-bins", "8", "--json"]) == 0
+    summary = _json.loads(capsys.readouterr().out)
+    for key in ("measured_sps", "avg_batch_ms", "avg_actor_ms", "total_batches", "total_actor_steps"):
+        assert key in summary
+    assert summary["total_actor_steps"] == 6 * 4
+
+    asset = gmdag.load_gmdag_asset(path)
+    h = bench_sdfdag.ObservationHarness(asset.nodes, asset.bbox_min, asset.bbox_max, 5, 32, 8, 30.0, 128)
+    seen = {}
+    real = h.res.cast_rays_poses
+
+    def spy(env_scene, local, pos, rot, *a, **k):
+        seen["pos"], seen["rot"] = pos.cpu().numpy().copy(), rot.cpu().numpy().copy()
+        return real(env_scene, local, pos, rot, *a, **k)
+
+    h.res.cast_rays_poses = spy
+    h.step()
+    prev0 = h.prev_depth.cpu().numpy().copy()  # the first step's depth
+    h.step()
+    torch.cuda.synchronize()
+    dirs = _rotate(oracle.ray_directions(32, 8), seen["rot"])
+    origins = np.ascontiguousarray(np.broadcast_to(seen["pos"][:, None, :], dirs.shape))
+    bmin, bmax = list(asset.bbox_min), list(asset.bbox_max)
+    ref = oracle.trace(asset.nodes, origins, dirs, 128, 30.0, bmin, bmax)
+    want = oracle.observe(ref["distance"], 32, 8, 30.0, semantics=ref["semantic"], prev_depth=prev0)
+    assert np.array_equal(h.out_d.cpu().numpy().view(np.uint32), ref["distance"].view(np.uint32))
+    go = h.obs.cpu().numpy()
+    np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
+    np.testing.assert_allclose(go[:, 0], want["obs"][:, 0], rtol=2.5e-7, atol=1e-7)
+    np.testing.assert_allclose(h.delta.cpu().numpy(), want["delta"], rtol=0, atol=3e-7)
+    np.testing.assert_allclose(h.stats.cpu().numpy()[:, 1:], want["stats"][:, 1:], atol=1e-6)
+    assert np.array_equal(h.stats.cpu().numpy()[:, 0], want["stats"][:, 0])
