@@ -204,7 +204,8 @@ def main() -> int:
     ap.add_argument("--scenes", type=int, default=16)
     ap.add_argument("--max-steps", type=int, default=256)
     ap.add_argument("--max-distance", type=float, default=30.0)
-    ap.add_argument("--cpu-envs", type=int, default=256, help="envs in the CPU-baseline sample")
+    ap.add_argument("--cpu-envs", type=int, default=1024,
+                    help="envs in the CPU-baseline sample (taken evenly over the scenes; all by default)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-raw", action="store_true", help="skip timing the reference-layout kernel")
     ap.add_argument("--obs-steps", type=int, default=128,
@@ -296,11 +297,17 @@ def main() -> int:
     cpu = None
     parity = None
     if not args.no_cpu:
-        sample = []
-        for s in range(len(corpus)):
-            idx = np.flatnonzero(env_scene == s)
-            sample.extend(idx[: max(1, args.cpu_envs // len(corpus))].tolist())
-        sample = np.array(sorted(sample)[: max(args.cpu_envs, len(corpus))])
+        if args.cpu_envs >= E:
+            sample = np.arange(E)
+            sample_text = f"the whole batch: {E} envs x {R} rays = {E * R} rays"
+        else:
+            per = max(1, args.cpu_envs // len(corpus))
+            sample = []
+            for s in range(len(corpus)):
+                sample.extend(np.flatnonzero(env_scene == s)[:per].tolist())
+            sample = np.array(sorted(sample)[: max(args.cpu_envs, len(corpus))])
+            sample_text = (f"{sample.size} envs x {R} rays = {sample.size * R} rays (the first {per} envs "
+                           f"of each of the {len(corpus)} scenes)")
         pool = np.concatenate([c.words for c in corpus])
         base = np.cumsum([0] + [c.words.size for c in corpus[:-1]]).astype(np.uint64)
         nw = np.array([c.words.size for c in corpus], np.uint64)
@@ -314,16 +321,14 @@ def main() -> int:
 
         ref = run_cpu()  # warm-up
         times = []
-        for _ in range(3):
+        for _ in range(2):
             t = time.perf_counter()
             run_cpu()
             times.append(time.perf_counter() - t)
         t_cpu = float(np.median(times))
         cpu = {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
                "kind": "port",
-               "sample": f"{sample.size} envs x {R} rays = {sample.size * R} rays (the first "
-                         f"{max(1, args.cpu_envs // len(corpus))} envs of each of the {len(corpus)} "
-                         f"scenes), median of 3 timed runs after 1 warm-up"}
+               "sample": f"{sample_text}, median of 2 timed runs after 1 warm-up"}
         gd = out_d.cpu().numpy()[sample]
         gs = out_s.cpu().numpy()[sample]
         gn = out_n.cpu().numpy()[sample]
