@@ -346,13 +346,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         const float px = __builtin_fmaf(t, dx, ox);
         const float py = __builtin_fmaf(t, dy, oy);
         const float pz = __builtin_fmaf(t, dz, oz);
+        // the cache tests in the reference's order, as exclusive outcomes:
+        // void cache (kernel.cu:265-267), outside the domain (:108-112), leaf
+        // cache (:114-118); one-leaf scenes always end here
         const bool hit_vd = vd_ok && in_box_strict(px, py, pz, vd);
-        const bool outside = !in_box(px, py, pz, dom);
-        const bool hit_lf = lf_ok && in_box(px, py, pz, lf);
+        const bool outside = !hit_vd && !in_box(px, py, pz, dom);
+        const bool hit_lf = !hit_vd && !outside && lf_ok && in_box(px, py, pz, lf);
         const bool use_pre = pre_ok && in_box(px, py, pz, pre);
-        const bool cached = hit_vd || outside || hit_lf;  // one-leaf scenes always hit here
-        bool descending = has_ray && !cached;
-        const bool did_descend = descending;
+        bool descending = has_ray && !(hit_vd || outside || hit_lf);
         Box cur;
         cur.x0 = use_pre ? pre.x0 : dom.x0;
         cur.y0 = use_pre ? pre.y0 : dom.y0;
@@ -451,16 +452,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         }
 
         // ---- classify the query result and update the caches ----
-        // (the shallow loop leaves `depth` at the table's value, <= 4: below the limit, as
-        // every slot of a shallow scene is)
-        const bool leaf_child = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at depth < 32
-        const bool is_void = hit_vd || (!cached && slot == kSlotVoid);
-        const bool is_leaf = !hit_vd && !outside && (hit_lf || (!cached && leaf_child));
-        // (shallow scenes carry no bad-child slots: navi_relayout and the root
-        // table turn them into faults, which they are at every depth < 32)
-        const bool is_fault = !cached && slot == kSlotFault;
-        const bool new_void = did_descend && is_void;
-        const bool new_leaf = !cached && is_leaf;  // from a descent
+        // Lanes that did not descend keep slot == 0 (an internal slot), so the
+        // descent outcomes below are false for them. (The shallow loop leaves
+        // `depth` at the table's value, <= 4: below the limit, as every slot of
+        // a shallow scene is. Shallow scenes carry no bad-child slots:
+        // navi_relayout and the root table turn them into faults, which they
+        // are at every depth < 32.)
+        const bool new_leaf = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at depth < 32
+        const bool new_void = slot == kSlotVoid;
+        const bool is_void = hit_vd || new_void;
+        const bool is_leaf = hit_lf || new_leaf;
+        const bool is_fault = slot == kSlotFault;
         vd.x0 = new_void ? cur.x0 : vd.x0;
         vd.y0 = new_void ? cur.y0 : vd.y0;
         vd.z0 = new_void ? cur.z0 : vd.z0;
@@ -502,14 +504,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         sem = is_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
         const bool hit = !is_fault && sem != 0 && dist < P.hit_eps;
         const float t_next = t + dist;
-        const bool done = has_ray && (is_fault || hit || t_next > P.max_distance || step >= P.max_steps);
+        // a finished ray reports t (NaN after a fault) and its semantic if it
+        // hit, else 0 (kernel.cu:297-308); the one write is after the leaf run
+        bool finish = has_ray && (is_fault || hit || t_next > P.max_distance || step >= P.max_steps);
         t = (has_ray && !hit) ? t_next : t;
-        if (done) {
-            P.out_d[ray] = is_fault ? __builtin_nanf("") : t;
-            P.out_s[ray] = hit ? sem : 0;
-            if (P.out_steps) P.out_steps[ray] = step;
-            has_ray = false;
-        }
+        t = (finish && is_fault) ? __builtin_nanf("") : t;
+        sem = (finish && !hit) ? 0 : sem;
+        has_ray = has_ray && !finish;
 
         // ---- further steps answered by the leaf cache alone ----
         // After a leaf step that neither hit nor ended the ray, the next point
@@ -538,13 +539,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 step += 1;
                 t = t + dist;
                 if (t > P.max_distance || step >= P.max_steps) {
-                    P.out_d[ray] = t;
-                    P.out_s[ray] = 0;
-                    if (P.out_steps) P.out_steps[ray] = step;
+                    finish = true;
+                    sem = 0;
                     has_ray = false;
                     run = false;
                 }
             }
+        }
+        if (finish) {
+            P.out_d[ray] = t;
+            P.out_s[ray] = sem;
+            if (P.out_steps) P.out_steps[ray] = step;
         }
     }
     // The last wave to finish rearms the queue for the next launch on this
