@@ -98,7 +98,8 @@ struct RelaidParams {
     float hit_eps;
     uint32_t n_chunks;
     uint32_t* __restrict__ queue;  // [next unit, finished waves], or null: static schedule
-    uint32_t n_units;              // kUnitRays-ray work units
+    uint32_t n_units;              // work units of unit_rays rays
+    uint32_t unit_rays;            // 256 (4 tiles), or 64 for batches too small to fill the chip
 };
 
 // Work index q -> ray id (env * R + r).
@@ -129,6 +130,7 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
 constexpr uint32_t kRefillMin = 8;
 constexpr uint32_t kLeafRun = 2;  // leaf-cache steps taken after a leaf step
 constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
+constexpr uint32_t kSmallUnitRays = 64;  // one tile, for small batches
 
 // A scene as the kernel reads it, staged in LDS once per workgroup so a lane
 // keeps only its scene index in registers.
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     const uint32_t seq_end = my_chunks * 64u;
     uint32_t seq_next = 0;  // wave-uniform
     // Dynamic schedule: units claimed from the queue, `unit_used` rays of `unit` handed out.
-    uint32_t unit = 0, unit_used = kUnitRays;
+    uint32_t unit = 0, unit_used = P.unit_rays;
     bool exhausted = (P.queue == nullptr) ? (seq_end == 0) : false;
 
     // per-lane ray state
@@ -253,19 +255,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 seq_next += n_need;
                 exhausted = seq_next >= seq_end;
             } else {
-                const uint32_t avail = kUnitRays - unit_used;
-                if (rank < avail) q = unit * kUnitRays + unit_used + rank;
+                const uint32_t avail = P.unit_rays - unit_used;
+                if (rank < avail) q = unit * P.unit_rays + unit_used + rank;
                 if (n_need > avail) {
                     uint32_t claimed = 0;
                     if (lane == 0) claimed = atomicAdd(P.queue, 1u);
                     claimed = __builtin_amdgcn_readlane(claimed, 0);
                     if (claimed < P.n_units) {
-                        if (rank >= avail) q = claimed * kUnitRays + (rank - avail);
+                        if (rank >= avail) q = claimed * P.unit_rays + (rank - avail);
                         unit = claimed;
                         unit_used = n_need - avail;
                     } else {
                         exhausted = true;
-                        unit_used = kUnitRays;
+                        unit_used = P.unit_rays;
                     }
                 } else {
                     unit_used += n_need;
@@ -605,7 +607,7 @@ uint32_t* queue_for(hipStream_t stream) {
 
 int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.n_chunks = (P.n_rays + 63u) / 64u;
-    P.n_units = (P.n_rays + kUnitRays - 1u) / kUnitRays;
+    P.unit_rays = kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
     const bool use_planes = P.n_scenes <= kPlaneScenes;
@@ -632,6 +634,11 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
         std::lock_guard<std::mutex> lock(g_queue_mu);
         g_grid_blocks[key] = grid_blocks;
     }
+    // Small batches: one-tile units, so that more waves get work (a launch
+    // wants several units per resident wave to balance the long rays).
+    if (static_cast<int64_t>(P.n_rays) < static_cast<int64_t>(kUnitRays) * 4 * 4 * grid_blocks)
+        P.unit_rays = kSmallUnitRays;
+    P.n_units = (P.n_rays + P.unit_rays - 1u) / P.unit_rays;
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
     if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;

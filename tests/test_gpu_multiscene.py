@@ -305,3 +305,28 @@ def test_bad_child_index_at_the_descent_limit(gpu, n):
     assert np.isnan(ref["distance"][0, 0]) == (n == 31)
     for kernel in ("raw", "relaid"):
         _compare(_run(res, np.zeros(1, np.int32), o, d, 6, 4.0, kernel=kernel), ref, 4.0, f"badchild{n}/{kernel}")
+
+
+def test_relaid_large_batch(gpu, corpus):
+    """A batch large enough for 256-ray work units (small batches use 64-ray
+    units): 1024 envs x 96x128 rays; every 31st env checked against the oracle."""
+    import torch
+
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    env_scene, o, d = _rays(corpus, 1024, 96, 128, seed=44)
+    dev = res.device
+    t_es = torch.from_numpy(env_scene).to(dev)
+    t_o, t_d = torch.from_numpy(o).to(dev), torch.from_numpy(d).to(dev)
+    out_d = torch.full(o.shape[:2], -7.0, device=dev)
+    out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+    out_n = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, 96, 30.0, out_steps=out_n, elevation_bins=128)
+    torch.cuda.synchronize()
+    assert int((out_n == -7).sum().item()) == 0
+    pick = np.arange(0, 1024, 31)
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene[pick], o[pick], d[pick], 96, 30.0)
+    got = (out_d.cpu().numpy()[pick], out_s.cpu().numpy()[pick], out_n.cpu().numpy()[pick], None)
+    _compare(got, ref, 30.0, "large")
