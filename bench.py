@@ -194,6 +194,46 @@ def dropin_timing(corpus, env_scene, t_o, t_d, args):
     return result
 
 
+def small_configs(dev):
+    """The smaller workloads of the benchmark definition, on the record-layout tracer:
+    they are latency-bound (too few rays to fill the chip), reported as ms per launch."""
+    import torch
+
+    from navi_amd import scenes as S
+    from navi_amd.multiscene import ResidentScenes
+
+    cases = [("1 env x 64x16 rays, box room @64^3, max 64 steps", S.box_room(seed=1, resolution=64), 1, 64, 16, 64),
+             ("4 envs x 256x48 rays, cluttered @128^3, max 128 steps", S.cluttered(seed=2, resolution=128), 4, 256,
+              48, 128),
+             ("64 envs x 256x48 rays, rooms @512^3, max 256 steps", S.rooms(seed=3, resolution=512), 64, 256, 48,
+              256)]
+    out = []
+    for name, sc, envs, az, el, max_steps in cases:
+        sc.compile()
+        res = ResidentScenes([(sc.words, sc.bbox_min_list, sc.bbox_max)], dev, keep_words=False)
+        rng = np.random.default_rng(envs)
+        origins = sc.free_origins(rng, envs)
+        dirs = S.world_directions(S.canonical_directions(az, el), rng.uniform(0, 2 * math.pi, envs))
+        o = torch.from_numpy(np.ascontiguousarray(np.broadcast_to(origins[:, None, :], dirs.shape))).to(dev)
+        d = torch.from_numpy(np.ascontiguousarray(dirs)).to(dev)
+        es = torch.zeros(envs, dtype=torch.int32, device=dev)
+        out_d = torch.empty(o.shape[:2], device=dev)
+        out_s = torch.empty(o.shape[:2], device=dev, dtype=torch.int32)
+        for _ in range(3):
+            res.cast_rays(es, o, d, out_d, out_s, max_steps, 30.0, elevation_bins=el)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(20):
+            res.cast_rays(es, o, d, out_d, out_s, max_steps, 30.0, elevation_bins=el)
+        ev1.record()
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / 20
+        out.append({"workload": name, "ms": round(ms, 4), "rays_per_s": round(envs * az * el / (ms / 1e3), 1)})
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,6 +387,7 @@ def main() -> int:
 
     obs = observation_steps(res, t_es, origins_env, yaw, E, args) if args.obs_steps > 0 else None
     dropin = dropin_timing(corpus, env_scene, t_o, t_d, args) if args.obs_steps > 0 else None
+    small = small_configs(dev) if args.obs_steps > 0 else None
 
     traffic = None
     tp = Path(args.traffic_profile)
@@ -394,6 +435,7 @@ def main() -> int:
         "parity": parity,
         "observation_step": obs,
         "dropin_cast_rays": dropin,
+        "small_configs": small,
         "scene_compile_s": round(t_compile, 2),
     }
     print(json.dumps(line), flush=True)
