@@ -142,7 +142,8 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * root_tables holds n_scenes * 4096 entries, scene s at s * 4096, from
  * navi_build_root_table). Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
- * (optional, a permutation of [0, n_envs)) is the order envs are swept in —
+ * (optional, a permutation of [0, n_envs); an entry outside that range is
+ * skipped, its rays left unwritten) is the order envs are swept in —
  * pass envs sorted by scene id so resident scenes stream through the caches
  * one at a time. elevation_bins > 0 (a multiple of 8 dividing rays_per_env / 8)
  * declares the canonical az*El + el ray layout (projects/environment/src/

@@ -4,28 +4,36 @@
 // checkout); tests compare both against the CPU oracle bit for bit.
 //
 // Execution model (CDNA4, wave64):
-//   * persistent waves: the grid holds about as many waves as the chip keeps
-//     resident; wave w walks 64-ray chunks w, w + W, w + 2W, ... of the work
-//     order, so all waves sweep the batch front to back together;
-//   * lane refill: at the top of every march step, lanes whose ray finished
-//     take the next rays of the wave's chunk sequence (ballot + prefix
-//     popcount), so a wave never idles on a few long rays;
-//   * one march step per outer iteration for every lane; the caches answer
-//     ~40% of steps with no memory traffic; the rest run a tight inner loop of
-//     one 4-byte gather per DAG level until every lane of the wave has found
-//     its leaf / void cell, then all lanes finish the step together;
+//   * persistent waves: the grid holds as many workgroups as the chip keeps
+//     resident; waves claim work units (256 rays = four 8 x 8 tiles, or one
+//     tile for batches too small to fill the chip) from a per-stream counter
+//     pair, the last wave rearming it; without a counter (more than 256
+//     streams) wave w takes 64-ray chunks w, w + W, ...;
+//   * lane refill: once 8 of 64 lanes have finished their rays, the idle lanes
+//     take the next rays (ballot + mbcnt rank), so a wave never idles on a few
+//     long rays;
+//   * one march step per outer iteration for every lane: the void / domain /
+//     leaf / prefix tests; a descent from the root locates its depth-4 cell
+//     (split planes staged in LDS, or four splits) and reads one root-table
+//     entry; then a per-lane loop reads one 4-byte slot per level until every
+//     lane of the wave has its leaf / void cell; then the step resolves with
+//     selects, and lanes whose step was a leaf take up to two more steps that
+//     the leaf cache answers alone;
 //   * work order: envs in the order given (callers sort them by scene so the
 //     resident scenes stream through L2 / MALL one or two at a time) and, when
 //     the elevation count is a multiple of 8, 8 x 8 (az x el) tiles of the
-//     canonical az*El + el ray layout, so a chunk's rays are angular
+//     canonical az*El + el ray layout, so a wave's rays are angular
 //     neighbours that share DAG nodes.
+// Launch-wide facts checked once per workgroup remove work without changing
+// results: `tame` scene boxes (coordinates below 2^100), `shallow` scenes (no
+// record deeper than 30 levels) and split planes close to a uniform grid.
 // Arithmetic: the void-cell exit divides (kernel.cu:54-85) use a per-ray
 // correctly rounded reciprocal and one Markstein correction,
 // q = fma(fma(-a*r, b, a), r, a*r), which equals the IEEE quotient a/b when
 // r = RN(1/b) and nothing over/underflows. Only quotients of at least 1e-5
 // can reach the result (the exit is clamped below at 1e-5), and for those,
-// with |b| > 1e-4 and box coordinates below 2^100, every intermediate is a
-// normal number; launches with larger coordinates take the IEEE division. 32-bit work indexing with
+// with |b| > 1e-4 and tame boxes, every intermediate is a normal number;
+// other launches take the IEEE division. 32-bit work indexing with
 // multiply-high division by the (uniform) rays-per-env and tile counts.
 #include <hip/hip_runtime.h>
 
@@ -79,6 +87,7 @@ struct RelaidParams {
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
     const int32_t* __restrict__ env_order;  // null: identity
     uint32_t n_rays;
+    uint32_t n_envs;
     uint32_t rays_per_env;
     FastDiv div_rays;      // by rays_per_env
     uint32_t tile_el;      // elevation bins when 8x8 tiling applies, else 0
@@ -273,9 +282,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     unit_used += n_need;
                 }
             }
-            if (!has_ray && q < P.n_rays) {
-                int32_t env;
-                ray = ray_of(P, q, env);
+            int32_t env = 0;
+            if (!has_ray && q < P.n_rays) ray = ray_of(P, q, env);
+            // env_order entries outside [0, n_envs) name no rays: skipped
+            if (!has_ray && q < P.n_rays && static_cast<uint32_t>(env) < P.n_envs) {
                 const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
                 if (kPoses) {
                     // sdfdag_backend.py:1300-1312: origin = the env's position;
@@ -683,6 +693,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     P.env_scene = env_scene;
     P.env_order = env_order;
     P.n_rays = static_cast<uint32_t>(n_rays);
+    P.n_envs = static_cast<uint32_t>(n_envs);
     P.rays_per_env = static_cast<uint32_t>(rays_per_env);
     P.div_rays = make_fastdiv(P.rays_per_env);
     P.tile_el = (elevation_bins > 0 && elevation_bins % 8 == 0 && rays_per_env % (8LL * elevation_bins) == 0)

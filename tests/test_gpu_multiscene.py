@@ -330,3 +330,35 @@ def test_relaid_large_batch(gpu, corpus):
                         env_scene[pick], o[pick], d[pick], 96, 30.0)
     got = (out_d.cpu().numpy()[pick], out_s.cpu().numpy()[pick], out_n.cpu().numpy()[pick], None)
     _compare(got, ref, 30.0, "large")
+
+
+def test_relaid_env_order_entries_out_of_range_are_skipped(gpu, corpus):
+    """A caller-built env_order with entries outside [0, n_envs): those work items
+    are skipped (their rays keep the sentinel), every named env is traced."""
+    import torch
+
+    from navi_amd import _native
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    env_scene, o, d = _rays(corpus, 6, 16, 8, seed=3)
+    dev = res.device
+    order = torch.tensor([5, 4, 99, 1, -3, 0], dtype=torch.int32, device=dev)  # envs 2 and 3 unnamed
+    t_es = torch.from_numpy(env_scene).to(dev)
+    t_o, t_d = torch.from_numpy(o).to(dev), torch.from_numpy(d).to(dev)
+    out_d = torch.full(o.shape[:2], -7.0, device=dev)
+    out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+    code = _native.lib().navi_trace_relaid(
+        res.records.data_ptr(), res.n_records, res.relaid_table.data_ptr(), res.n_scenes,
+        res.root_tables.data_ptr(), t_es.data_ptr(), order.data_ptr(), 6, 16 * 8, 8, t_o.data_ptr(),
+        t_d.data_ptr(), out_d.data_ptr(), out_s.data_ptr(), 64, 30.0, 0.01, None,
+        torch.cuda.current_stream().cuda_stream)
+    _native.check(code)
+    torch.cuda.synchronize()
+    gd = out_d.cpu().numpy()
+    assert (gd[[2, 3]] == -7.0).all()
+    named = [0, 1, 4, 5]
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene[named], o[named], d[named], 64, 30.0)
+    assert np.array_equal(gd[named].view(np.uint32), ref["distance"].view(np.uint32))
+    assert np.array_equal(out_s.cpu().numpy()[named], ref["semantic"])
