@@ -362,3 +362,47 @@ def test_relaid_env_order_entries_out_of_range_are_skipped(gpu, corpus):
                         env_scene[named], o[named], d[named], 64, 30.0)
     assert np.array_equal(gd[named].view(np.uint32), ref["distance"].view(np.uint32))
     assert np.array_equal(out_s.cpu().numpy()[named], ref["semantic"])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_relaid_randomized_sweep(gpu, seed):
+    """Seeded random scenes (box room / cluttered / rooms at 32..256), shifted and
+    scaled domains, random hit epsilons and step budgets, rays from inside and
+    outside the domains in random directions: the record-layout tracer against
+    the oracle."""
+    import torch
+
+    from navi_amd import scenes as S
+    from navi_amd.multiscene import ResidentScenes
+
+    rng = np.random.default_rng(1000 + seed)
+    makers = [lambda s, r: S.box_room(seed=s, resolution=r), lambda s, r: S.cluttered(seed=s, resolution=r),
+              lambda s, r: S.rooms(seed=s, resolution=r, grid=3)]
+    scenes = []
+    for k in range(3):
+        sc = makers[int(rng.integers(0, 3))](int(rng.integers(0, 10_000)), int(rng.choice([32, 64, 128, 256])))
+        words = sc.compile()
+        # the same DAG over another domain: shift and scale the cube
+        scale = float(rng.choice([1.0, 0.37, 3.3]))
+        shift = rng.uniform(-50, 50, 3)
+        lo = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_min_list, shift)]
+        hi = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_max, shift)]
+        scenes.append((words, lo, hi))
+    res = ResidentScenes(scenes)
+    n_env, rays = 9, 700
+    env_scene = rng.integers(0, 3, n_env).astype(np.int32)
+    lo = np.array([scenes[s][1] for s in env_scene], np.float64)
+    hi = np.array([scenes[s][2] for s in env_scene], np.float64)
+    span = hi - lo
+    o = rng.uniform(lo[:, None, :] - 0.1 * span[:, None, :], hi[:, None, :] + 0.1 * span[:, None, :],
+                    (n_env, rays, 3)).astype(np.float32)
+    d = rng.normal(size=(n_env, rays, 3))
+    d[:, :50, 1] = 0.0  # some rays in the horizontal plane
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    max_steps = int(rng.integers(1, 300))
+    max_distance = float(np.float32(rng.uniform(1.0, 60.0)))
+    eps = float(np.float32(rng.choice([0.01, 1e-3, 0.05])))
+    ref = _oracle_multi([s[0] for s in scenes], [s[1] + s[2] for s in scenes], env_scene, o, d, max_steps,
+                        max_distance, hit_epsilon=eps)
+    _compare(_run(res, env_scene, o, d, max_steps, max_distance, hit_epsilon=eps), ref, max_distance,
+             f"sweep{seed}")
