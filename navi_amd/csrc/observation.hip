@@ -20,6 +20,11 @@
 #include "navi_trace.h"
 #include "trace_common.hpp"
 
+// v_rcp_f32: within one ulp of the correctly rounded reciprocal
+__device__ inline float navi_recip(float b) { return __builtin_amdgcn_rcpf(b); }
+#define NAVI_MATH_FN __device__ inline
+#include "log1p_nonneg.h"
+
 namespace navi {
 
 int set_error(int code, const char* fmt, ...);
@@ -29,7 +34,7 @@ namespace {
 constexpr uint32_t kSlotVoid = 0x7fffffffu;
 constexpr uint32_t kSlotFault = 0x7ffffffeu;
 constexpr uint32_t kSlotBadChild = 0x7ffffffdu;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr float kVoidClearance = 1.7321f;  // compiler.cpp:626,639-643: pruned octants clear half-diagonal
 
 enum : int32_t { kKindOutside = 0, kKindLeaf = 1, kKindVoid = 2, kKindDepth = 3, kKindFault = 4 };
@@ -39,8 +44,10 @@ struct PostParams {
     int32_t n_envs;
     // The reference compares float32 tensors with Python floats and divides
     // by one: the host rounds max_distance - 1e-3 and log1p(max_distance),
-    // evaluated in double, to float, as torch does with such scalars.
-    float saturation, log_denom;
+    // evaluated in double, to float, as torch does with such scalars. torch
+    // divides a float32 device tensor by such a scalar as a multiplication by
+    // its float reciprocal: inv_log_denom = RN(1 / RN(log1p(max_distance))).
+    float saturation, inv_log_denom;
     int32_t stage16;  // stage the transposed fp16 tile in LDS (n halves fit)
     // point queries
     const uint32_t* __restrict__ records;
@@ -134,17 +141,15 @@ __device__ T block_sum(T v, T* lds) {
     return r;
 }
 
-// torch.amin semantics: NaN if any input is NaN.
-__device__ float nan_min(float a, float b) { return (a != a || b != b) ? __builtin_nanf("") : fminf(a, b); }
-
+// minimum over the workgroup of values that are not NaN
 __device__ float block_min(float v, float* lds) {
-    for (int off = 32; off > 0; off >>= 1) v = nan_min(v, __shfl_xor(v, off));
+    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off));
     const int w = threadIdx.x >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) lds[w] = v;
     __syncthreads();
     float r = lds[0];
-    for (int k = 1; k < kThreads / 64; ++k) r = nan_min(r, lds[k]);
+    for (int k = 1; k < kThreads / 64; ++k) r = fminf(r, lds[k]);
     return r;
 }
 
@@ -171,26 +176,33 @@ __global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
         for (int32_t k = threadIdx.x; k < n; k += kThreads) acc += fabsf(O.prev_depth[base + k]);
         first = block_sum(acc, lds_f) < 1e-6f;
     }
-    // sdfdag_backend.py:390: the first and last Az/6 azimuth bins (at least one)
+    // sdfdag_backend.py:390: the first and last Az/6 azimuth bins (at least
+    // one), i.e. flat indices k < fwd_lo and k >= fwd_hi
     const int32_t fwd = max(1, az / 6);
+    const int32_t fwd_lo = fwd * el, fwd_hi = (az - fwd) * el;
     const bool band = O.structure_band_max > O.structure_band_min;
-    uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0;
-    float mn = INFINITY;
-    for (int32_t k = threadIdx.x; k < n; k += kThreads) {
-        const float m = dist[k];
+    uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0, n_nan = 0;
+    float mn = INFINITY;  // of the clamped values that are not NaN
+    // Element k = a * El + r (azimuth bin a, elevation bin r) sits at t = r * Az + a
+    // in the transposed fp16 depth. Counters use & rather than && so that
+    // they stay branch-free.
+    auto element = [&](int32_t k, int32_t t, float m) {
         const bool valid = isfinite(m);
-        // torch.clamp(min=0, max=max_distance): NaN stays NaN
-        const float c = (m != m) ? m : fminf(fmaxf(m, 0.0f), O.max_distance);
-        mn = nan_min(mn, c);
-        n_sat += (c >= P.saturation) ? 1u : 0u;
-        n_prox += (valid && c <= O.proximity_threshold) ? 1u : 0u;
-        const bool in_band = band && valid && c >= O.structure_band_min && c <= O.structure_band_max;
-        n_band += in_band ? 1u : 0u;
-        const int32_t a = k / el;
+        const bool nan = m != m;
+        // torch.clamp(min=0, max=max_distance): both compares are false for NaN
+        float c = m < 0.0f ? 0.0f : m;
+        c = c > O.max_distance ? O.max_distance : c;
+        mn = fminf(mn, c);
+        n_nan += nan;
+        n_sat += c >= P.saturation;
+        n_prox += valid & (c <= O.proximity_threshold);
+        const bool in_band = band & valid & (c >= O.structure_band_min) & (c <= O.structure_band_max);
+        n_band += in_band;
         // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
-        n_fwd += in_band ? static_cast<uint32_t>((a < fwd ? 1 : 0) + (a >= az - fwd ? 1 : 0)) : 0u;
-        // sdfdag_backend.py:441-443
-        const float q = c != c ? c : fminf(fmaxf(log1pf(c) / P.log_denom, 0.0f), 1.0f);
+        n_fwd += static_cast<uint32_t>(in_band & (k < fwd_lo)) + static_cast<uint32_t>(in_band & (k >= fwd_hi));
+        // sdfdag_backend.py:441-443; c >= 0 here, so the log1p of non-negative
+        // arguments applies (within one ulp of the exact log1p)
+        const float q = nan ? c : fminf(fmaxf(navi_log1p_nonneg(c) * P.inv_log_denom, 0.0f), 1.0f);
         if (O.obs) {  // sdfdag_backend.py:1516-1524: stack(depth, semantic, valid), (Az, El) order
             float* ob = O.obs + 3 * base;
             ob[k] = q;
@@ -203,12 +215,40 @@ __global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
             O.prev_depth[base + k] = q;
         }
         if (O.depth_f16) {
-            const int32_t t = (k - a * el) * az + a;  // transposed: (El, Az)
             if (P.stage16) {
                 lds16[t] = static_cast<_Float16>(q);
             } else {
                 static_cast<_Float16*>(O.depth_f16)[base + t] = static_cast<_Float16>(q);
             }
+        }
+    };
+    // kBatch coalesced loads in flight per thread before any is used. One
+    // division per batch; then k advances by kThreads = da * El + dr, i.e. r by
+    // dr and t by dr * Az + da, with a carry of one azimuth bin when r wraps.
+    constexpr int32_t kBatch = 8;
+    const int32_t da = kThreads / el, dr = kThreads - da * el;
+    const int32_t dt = dr * az + da, wrap = 1 - el * az;
+    for (int32_t k0 = threadIdx.x; k0 < n; k0 += kThreads * kBatch) {
+        float m[kBatch];
+#pragma unroll
+        for (int32_t j = 0; j < kBatch; ++j) {
+            const int32_t k = k0 + j * kThreads;
+            m[j] = k < n ? dist[k] : 0.0f;
+        }
+        const int32_t a0 = k0 / el;
+        int32_t r = k0 - a0 * el, t = r * az + a0;
+#pragma unroll
+        for (int32_t j = 0; j < kBatch; ++j) {
+            const int32_t k = k0 + j * kThreads;
+            if (k < n) element(k, t, m[j]);
+            r += dr;
+            t += dt;
+            if (r >= el) {
+                r -= el;
+                t += wrap;
+            }
+            // keep the running (r, t): recomputing them from k costs integer multiplies
+            asm volatile("" : "+v"(r), "+v"(t));
         }
     }
     if (O.depth_f16 && P.stage16) {
@@ -221,7 +261,9 @@ __global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
     n_prox = block_sum(n_prox, lds_u);
     n_band = block_sum(n_band, lds_u);
     n_fwd = block_sum(n_fwd, lds_u);
+    n_nan = block_sum(n_nan, lds_u);
     mn = block_min(mn, lds_f);
+    if (n_nan != 0) mn = __builtin_nanf("");  // torch.amin: NaN if any input is NaN
     if (threadIdx.x == 0) {
         const float fn = static_cast<float>(n);
         if (O.stats) {
@@ -298,7 +340,7 @@ extern "C" int navi_observe(const navi_observation* observation, const navi_poin
         P.n_envs = static_cast<int32_t>(O.n_envs);
         P.env_blocks = P.n_envs;
         P.saturation = static_cast<float>(static_cast<double>(O.max_distance) - 1e-3);
-        P.log_denom = static_cast<float>(std::log1p(static_cast<double>(O.max_distance)));
+        P.inv_log_denom = 1.0f / static_cast<float>(std::log1p(static_cast<double>(O.max_distance)));
         const int64_t n = static_cast<int64_t>(O.azimuth_bins) * O.elevation_bins;
         // a 48 KiB tile at most, and an even count for the 4-byte copy out
         P.stage16 = (O.depth_f16 != nullptr && n % 2 == 0 && n * 2 <= 48 * 1024) ? 1 : 0;

@@ -4,8 +4,8 @@ queries (navi_point_query) and the fused post-pass (navi_observe).
 
 Bars: traced rays as in test_gpu_multiscene (bit-exact); point queries
 bit-exact (distance bits, semantic, kind); post-pass min distance and
-collision exact, ratios within 1e-6, fp16 depth within one binary16 ulp
-(torch CPU log1p versus the device's log1pf).
+collision exact, ratios within 1e-6, fp16 depth within one binary16 ulp,
+float32 depth within DEPTH_RTOL of the oracle's.
 """
 
 from __future__ import annotations
@@ -19,6 +19,15 @@ import oracle
 from tests.test_gpu_multiscene import _compare, _corpus, _oracle_multi, _run
 
 pytestmark = pytest.mark.gpu
+
+# The float32 depth q = log1p(c) / log1p(max) against the oracle's: the
+# device's is within 2.31e-7 relative of the exact value (its log1p within
+# 0.92 ulp, checked on the host for every float in [0, 32] by
+# tests/native/log1p_check.c; then RN(1 / log1p(max)) and the product round
+# once each), the oracle's (torch CPU log1p within one ulp, one division)
+# within 1.8e-7: 4.2e-7 between them. q <= 1, so the same bound is absolute
+# for the delta of two frames that start from the same previous depth.
+DEPTH_RTOL = 4.2e-7
 
 
 @pytest.fixture(scope="module")
@@ -195,18 +204,56 @@ def test_observe_matches_oracle(gpu, corpus, az, el, band):
                 out_stats=st, out_collision=co, semantics=ts, out_obs=obs, prev_depth=tprev, out_delta=delta)
     torch.cuda.synchronize()
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
-    # float32 outputs: depth within 2 ulp (log1pf versus torch CPU), semantic / valid exact
+    # float32 outputs: depth within DEPTH_RTOL, semantic / valid exact
     go = obs.cpu().numpy()
     np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
     wd = want["obs"][:, 0]
     assert np.array_equal(np.isnan(go[:, 0]), np.isnan(wd))
-    np.testing.assert_allclose(np.nan_to_num(go[:, 0]), np.nan_to_num(wd), rtol=2.5e-7, atol=1e-7)
+    np.testing.assert_allclose(np.nan_to_num(go[:, 0]), np.nan_to_num(wd), rtol=DEPTH_RTOL, atol=1e-7)
     gdel = delta.cpu().numpy()
     assert (gdel[3] == 0).all()
     assert np.array_equal(np.isnan(gdel), np.isnan(want["delta"]))
-    np.testing.assert_allclose(np.nan_to_num(gdel), np.nan_to_num(want["delta"]), rtol=0, atol=3e-7)
+    np.testing.assert_allclose(np.nan_to_num(gdel), np.nan_to_num(want["delta"]), rtol=0, atol=DEPTH_RTOL)
     # prev_depth now holds the depth
     assert np.array_equal(tprev.cpu().numpy().view(np.uint32), go[:, 0].view(np.uint32))
+
+
+def test_observe_depth_against_exact_log1p(gpu, corpus):
+    """The normalised depth over every 531st binary32 in [0, 30] (every binade,
+    subnormals included) against log1p(c) / log1p(30) in float64: float32 within
+    2.31e-7 relative (the bound in DEPTH_RTOL's comment) plus half the smallest
+    subnormal, fp16 within one binary16 ulp of the exact value rounded to
+    binary16. Pins the device log1p and reciprocal on the hardware itself."""
+    import torch
+
+    az, el = 64, 16
+    top = int(np.float32(30.0).view(np.uint32))
+    bits = np.arange(0, top + 1, 531, dtype=np.uint32)
+    special = np.array([0.0, 30.0, 2.0 ** -24, np.nextafter(np.float32(2.0 ** -24), 1), 1.0, 29.999998],
+                       np.float32).view(np.uint32)
+    bits = np.concatenate([bits, special])
+    n_envs = -(-bits.size // (az * el))
+    c = np.ones(n_envs * az * el, np.float32)
+    c[: bits.size] = bits.view(np.float32)
+    c = c.reshape(n_envs, az * el)
+    res = _resident(corpus)
+    dev = res.device
+    td = torch.from_numpy(c).to(dev)
+    sem = torch.zeros((n_envs, az * el), dtype=torch.int32, device=dev)
+    obs = torch.empty((n_envs, 3, az, el), device=dev)
+    d16 = torch.empty((n_envs, 1, el, az), dtype=torch.float16, device=dev)
+    res.observe(td, az, el, 30.0, semantics=sem, out_obs=obs, out_depth_f16=d16)
+    torch.cuda.synchronize()
+    q = obs[:, 0].cpu().numpy().reshape(-1).astype(np.float64)
+    exact = np.log1p(c.reshape(-1).astype(np.float64)) / math.log1p(30.0)
+    err = np.abs(q - exact)
+    bound = 2.31e-7 * exact + 2.0 ** -150
+    worst = int(np.argmax(err / bound))
+    assert (err <= bound).all(), f"c={c.reshape(-1)[worst]!r}: {q[worst]!r} vs {exact[worst]!r}"
+    h = d16.cpu().numpy().transpose(0, 1, 3, 2).reshape(-1).astype(np.float64)
+    h_exact = exact.astype(np.float16)
+    ulp = np.spacing(h_exact).astype(np.float64)
+    assert (np.abs(h - h_exact.astype(np.float64)) <= ulp).all()
 
 
 def test_observation_step_end_to_end(gpu, corpus):
@@ -291,7 +338,7 @@ def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
     assert np.array_equal(h.out_d.cpu().numpy().view(np.uint32), ref["distance"].view(np.uint32))
     go = h.obs.cpu().numpy()
     np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
-    np.testing.assert_allclose(go[:, 0], want["obs"][:, 0], rtol=2.5e-7, atol=1e-7)
-    np.testing.assert_allclose(h.delta.cpu().numpy(), want["delta"], rtol=0, atol=3e-7)
+    np.testing.assert_allclose(go[:, 0], want["obs"][:, 0], rtol=DEPTH_RTOL, atol=1e-7)
+    np.testing.assert_allclose(h.delta.cpu().numpy(), want["delta"], rtol=0, atol=DEPTH_RTOL)
     np.testing.assert_allclose(h.stats.cpu().numpy()[:, 1:], want["stats"][:, 1:], atol=1e-6)
     assert np.array_equal(h.stats.cpu().numpy()[:, 0], want["stats"][:, 0])
