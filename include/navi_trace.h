@@ -122,16 +122,23 @@ typedef struct navi_relaid_scene {
 int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root_slot, uint32_t* max_depth);
 
 /*
- * Root table of one scene (no reference counterpart; host memory in and out):
- * 4096 u64 entries over the 16 x 16 x 16 grid of depth-4 cells. Entry
- * (iz * 16 + iy) * 16 + ix (the cell whose octant at depth l has x bit
- * (ix >> (3 - l)) & 1, y and z likewise) = the slot a descent from the root
- * meets within four levels (bits 31..0: a leaf, void or out-of-range slot, or
- * the record of the internal node at depth 4) | its depth (bits 34..32; 0 for
- * a one-leaf DAG). Pass the scene's records and root_slot as the tracer sees
- * them (absolute record indices in a pool), so record slots in the table are
- * absolute too.
+ * Cell table of one scene (no reference counterpart; host memory in and out):
+ * 8^depth u64 entries over the 2^depth x 2^depth x 2^depth grid of the cells
+ * at that depth, depth in [4, 7]. Entry (iz << 2 depth) | (iy << depth) | ix
+ * (the cell whose octant at level l has x bit (ix >> (depth - 1 - l)) & 1, y
+ * and z likewise) = the slot a descent from the root meets within `depth`
+ * levels (bits 31..0: a leaf, void or out-of-range slot, or the record of the
+ * internal node at that depth) | its depth (bits 34..32; 0 for a one-leaf
+ * DAG). Pass the scene's records and root_slot as the tracer sees them
+ * (absolute record indices in a pool), so record slots in the table are
+ * absolute too. The tracer's descents start at the table's depth: deeper
+ * tables save record reads and cost 8x the memory per level (depth 6: 2 MiB
+ * per scene).
  */
+int navi_build_cell_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot, int32_t depth,
+                          uint64_t* out_table);
+
+/* navi_build_cell_table at depth 4: 4096 entries. */
 int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
                           uint64_t* out_table);
 
@@ -139,8 +146,9 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
  * traces scenes[env_scene ? env_scene[e] : 0] (at most 1024 scenes; `records`
  * holds n_records records with absolute child slots, see navi_relaid_scene;
- * root_tables holds n_scenes * 4096 entries, scene s at s * 4096, from
- * navi_build_root_table). Per-ray results are identical
+ * root_tables holds n_scenes cell tables of depth table_depth, 8^table_depth
+ * entries each, scene s at s * 8^table_depth, from navi_build_cell_table).
+ * Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
  * (optional, a permutation of [0, n_envs); an entry outside that range is
  * skipped, its rays left unwritten) is the order envs are swept in —
@@ -151,7 +159,7 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
  */
 int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                      int32_t n_scenes, const uint64_t* root_tables,
+                      int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
                       const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                       int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                       const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -171,7 +179,8 @@ int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_re
  * cos / sin values. Everything else as navi_trace_relaid.
  */
 int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                            int32_t n_scenes, const uint64_t* root_tables, const int32_t* env_scene,
+                            int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
+                            const int32_t* env_scene,
                             const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
                             int32_t elevation_bins, const float* local_dirs, const float* env_pos,
                             const float* env_rot, float* out_distances, int32_t* out_semantics,
@@ -184,7 +193,8 @@ typedef struct navi_point_queries {
     uint64_t n_records;
     const navi_relaid_scene* scenes;
     int32_t n_scenes;
-    const uint64_t* root_tables;
+    const uint64_t* root_tables;       /* cell tables as in navi_trace_relaid */
+    int32_t table_depth;
     const int32_t* point_scene;        /* [n_points] scene ids, or NULL: scene 0 */
     const float* points;               /* [n_points][3] */
     int64_t n_points;

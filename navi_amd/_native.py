@@ -54,17 +54,19 @@ _lib.navi_relayout.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p
 _lib.navi_trace_relaid.restype = ctypes.c_int
 _lib.navi_build_root_table.restype = ctypes.c_int
 _lib.navi_build_root_table.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _vp]
+_lib.navi_build_cell_table.restype = ctypes.c_int
+_lib.navi_build_cell_table.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int32, _vp]
 _lib.navi_record_depth.restype = ctypes.c_int
 _lib.navi_record_depth.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _u32p]
 _lib.navi_trace_relaid.argtypes = [
-    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp, _vp,
-    _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
+    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+    ctypes.c_int32, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 
 _lib.navi_trace_relaid_poses.restype = ctypes.c_int
 _lib.navi_trace_relaid_poses.argtypes = [
-    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, _vp,
-    _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
+    _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
+    ctypes.c_int32, _vp, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 
 
@@ -72,7 +74,8 @@ class PointQueries(ctypes.Structure):
     """navi_point_queries (include/navi_trace.h)."""
 
     _fields_ = [("records", _vp), ("n_records", ctypes.c_uint64), ("scenes", _vp), ("n_scenes", ctypes.c_int32),
-                ("root_tables", _vp), ("point_scene", _vp), ("points", _vp), ("n_points", ctypes.c_int64),
+                ("root_tables", _vp), ("table_depth", ctypes.c_int32), ("point_scene", _vp), ("points", _vp),
+                ("n_points", ctypes.c_int64),
                 ("out_distances", _vp), ("out_semantics", _vp), ("out_kind", _vp)]
 
 
@@ -124,6 +127,18 @@ def root_table(records, root_slot):
     out = np.zeros(4096, np.uint64)
     check(_lib.navi_build_root_table(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
                                      out.ctypes.data))
+    return out
+
+
+def cell_table(records, root_slot, depth):
+    """Host cell table of one scene at ``depth`` in [4, 7] (``navi_build_cell_table``):
+    uint64 [8**depth]."""
+    import numpy as np
+
+    rec = np.ascontiguousarray(records, dtype=np.uint32).reshape(-1, 8)
+    out = np.zeros(8 ** int(depth) if 4 <= int(depth) <= 7 else 1, np.uint64)
+    check(_lib.navi_build_cell_table(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
+                                     int(depth), out.ctypes.data))
     return out
 
 

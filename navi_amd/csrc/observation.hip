@@ -11,8 +11,8 @@
 // (env, 1, El, Az), the layout the policy consumes.
 //
 // Point queries: one lane per point, a fresh descent with no caches (the
-// query of kernel.cu:88-200 from the root): the root table gives the first
-// four levels, record reads the rest.
+// query of kernel.cu:88-200 from the root): the cell table gives the first
+// D levels, record reads the rest.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -54,7 +54,8 @@ struct PostParams {
     uint32_t n_records;
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
-    const uint64_t* __restrict__ root_table;
+    const uint64_t* __restrict__ root_table;  // cell tables, 8^table_depth entries per scene
+    uint32_t table_depth;
     const int32_t* __restrict__ point_scene;  // [n_points] or null (scene 0)
     const float* __restrict__ points;         // [n_points][3]
     int32_t n_points;
@@ -83,20 +84,21 @@ __device__ void point_query(const PostParams& P, int32_t i) {
             uint32_t slot = S.root_slot;
             int32_t depth = 0;
             if (!(slot & 0x80000000u)) {
+                const uint32_t D = P.table_depth;
                 uint32_t jx = 0, jy = 0, jz = 0;
-                for (int l = 0; l < kPrefixDepth; ++l) {
+                for (uint32_t l = 0; l < D; ++l) {
                     const uint32_t oct = descend_octant(px, py, pz, cur);
                     jx = 2u * jx + (oct & 1u);
                     jy = 2u * jy + ((oct >> 1) & 1u);
                     jz = 2u * jz + (oct >> 2);
                 }
-                const uint64_t e = P.root_table[((((uint32_t)sc << 4 | jz) << 4 | jy) << 4) | jx];
+                const uint64_t e = P.root_table[((((uint32_t)sc << D | jz) << D | jy) << D) | jx];
                 slot = static_cast<uint32_t>(e);
                 depth = static_cast<int32_t>(e >> 32);
-                if (depth < kPrefixDepth) {
+                if (depth < static_cast<int32_t>(D)) {
                     cur = dom;
                     for (int32_t l = 0; l < depth; ++l) {
-                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        const uint32_t b = D - 1u - static_cast<uint32_t>(l);
                         split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
                     }
                 }
@@ -296,12 +298,14 @@ int points_setup(PostParams& P, const navi_point_queries* Q) {
         return set_error(NAVI_E_ARG, "points and point outputs must be non-null");
     if (Q->n_scenes <= 0 || !Q->scenes || !Q->records || !Q->root_tables)
         return set_error(NAVI_E_ARG, "scene table, records and root_tables must be non-empty");
+    if (Q->table_depth < 4 || Q->table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (Q->n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
     P.records = Q->records;
     P.n_records = static_cast<uint32_t>(Q->n_records);
     P.scenes = Q->scenes;
     P.n_scenes = Q->n_scenes;
     P.root_table = Q->root_tables;
+    P.table_depth = static_cast<uint32_t>(Q->table_depth);
     P.point_scene = Q->point_scene;
     P.points = Q->points;
     P.n_points = static_cast<int32_t>(Q->n_points);

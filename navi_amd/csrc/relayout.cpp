@@ -185,37 +185,61 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
     return NAVI_OK;
 }
 
-// Root table: what a descent from the root reaches within the first four
-// levels (kernel.cu:136-199 stops at a leaf or void cell; the prefix cache of
-// kernel.cu:154-163 keys on the internal node met at depth 4). The depth-4
-// cells form a 16 x 16 x 16 grid; entry (iz * 16 + iy) * 16 + ix holds, for
-// the cell whose octant at depth l has x bit (ix >> (3 - l)) & 1 (y, z
+namespace {
+
+// Cells of the block a slot covers at depth d: a terminal slot (leaf, void,
+// fault, bad child) above depth D, or the slot met at depth D, fills its
+// (2^(D-d))^3 cells; an internal slot above depth D recurses into its
+// octants (x bit 0, y bit 1, z bit 2: the upper half along an axis holds the
+// points >= the midpoint, kernel.cu:165-176).
+void fill_cells(const uint32_t* records, uint64_t n_records, uint32_t slot, uint32_t d, uint32_t D,
+                uint32_t x0, uint32_t y0, uint32_t z0, uint64_t* out) {
+    if (d == D || slot >= kSlotBadChild) {
+        // a bad child index examined above depth 32 is a fault
+        const uint32_t s = slot == kSlotBadChild ? kSlotFault : slot;
+        const uint64_t v = static_cast<uint64_t>(s) | (static_cast<uint64_t>(d) << 32);
+        const uint32_t w = 1u << (D - d);
+        for (uint32_t z = z0; z < z0 + w; ++z)
+            for (uint32_t y = y0; y < y0 + w; ++y) {
+                uint64_t* row = out + ((static_cast<uint64_t>(z) << D | y) << D);
+                for (uint32_t x = x0; x < x0 + w; ++x) row[x] = v;
+            }
+        return;
+    }
+    const uint32_t half = 1u << (D - d - 1);
+    for (uint32_t oct = 0; oct < 8u; ++oct) {
+        const uint32_t child = static_cast<uint64_t>(slot) < n_records ? records[8ull * slot + oct] : kSlotFault;
+        fill_cells(records, n_records, child, d + 1, D, x0 + (oct & 1u) * half, y0 + ((oct >> 1) & 1u) * half,
+                   z0 + (oct >> 2) * half, out);
+    }
+}
+
+}  // namespace
+
+// Cell table: what a descent from the root reaches within the first D
+// levels (kernel.cu:136-199 stops at a leaf or void cell). The depth-D cells
+// form a 2^D x 2^D x 2^D grid; entry (iz << 2D) | (iy << D) | ix holds, for the
+// cell whose octant at depth l has x bit (ix >> (D - 1 - l)) & 1 (y, z
 // likewise), the slot met and, in bits 32..34, its depth d: a leaf / void /
-// fault slot at d <= 4, or the record of the internal node at d = 4. Only
+// fault slot at d <= D, or the record of the internal node at d = D. Only
 // octant bits are involved, so a tracer that locates the cell itself and
-// reads one entry follows the same path as four record reads. A one-leaf DAG
-// maps every entry to its root leaf at depth 0.
-extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
-                                     uint64_t* out_table) {
+// reads one entry follows the same path as D record reads; the depth-4 node
+// on that path (the prefix cache of kernel.cu:154-163) is internal exactly
+// when d > 4, or d = 4 and the slot is a record. A one-leaf DAG maps every
+// entry to its root leaf at depth 0.
+extern "C" int navi_build_cell_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                                     int32_t depth, uint64_t* out_table) {
     using navi::set_error;
     if (!out_table || (!records && n_records)) return set_error(NAVI_E_ARG, "null argument");
-    for (uint32_t c = 0; c < 4096u; ++c) {
-        uint32_t slot = root_slot, d = 0;
-        if (!(root_slot & 0x80000000u)) {
-            uint32_t r = root_slot;
-            for (uint32_t l = 0; l < 4u; ++l) {
-                const uint32_t b = 3u - l;
-                const uint32_t oct = ((c >> b) & 1u) | (((c >> (4u + b)) & 1u) << 1) | (((c >> (8u + b)) & 1u) << 2);
-                slot = static_cast<uint64_t>(r) < n_records ? records[8ull * r + oct] : kSlotFault;
-                d = l + 1u;
-                if (slot >= kSlotBadChild || d == 4u) break;
-                r = slot;
-            }
-        }
-        if (slot == kSlotBadChild) slot = kSlotFault;  // examined at depth <= 4: a fault
-        out_table[c] = static_cast<uint64_t>(slot) | (static_cast<uint64_t>(d) << 32);
-    }
+    if (depth < 4 || depth > 7) return set_error(NAVI_E_ARG, "table depth must be in [4, 7]");
+    fill_cells(records, n_records, root_slot, 0u, static_cast<uint32_t>(depth), 0u, 0u, 0u, out_table);
     return NAVI_OK;
+}
+
+// The cell table of depth 4 (4096 entries).
+extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                                     uint64_t* out_table) {
+    return navi_build_cell_table(records, n_records, root_slot, 4, out_table);
 }
 
 // Longest chain of internal records below the root, in levels: the deepest

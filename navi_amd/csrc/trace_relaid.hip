@@ -83,7 +83,8 @@ struct RelaidParams {
     uint32_t n_records;  // records in the pool (child slots are absolute indices)
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
-    const uint64_t* __restrict__ root_table;  // 4096 entries per scene
+    const uint64_t* __restrict__ root_table;  // cell tables, 8^cell_depth entries per scene
+    uint32_t cell_depth;                      // D in [4, 7]: descents start at depth D
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
     const int32_t* __restrict__ env_order;  // null: identity
     uint32_t n_rays;
@@ -149,52 +150,64 @@ struct SceneLds {
     uint32_t pad;
 };
 constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
-// Split planes of the first four levels, per scene and axis: the 17 planes
-// P_0 = lo, ..., P_16 = hi of the 16 depth-4 cells, then 16 / (hi - lo).
-constexpr int32_t kPlaneStride = 18;
-constexpr int32_t kPlaneScenes = 64;  // launches with more scenes skip the planes (LDS budget)
+// Split planes of the first D levels, per scene: the scales n / (hi - lo) of
+// x, y and z and a pad float, then per axis the n + 1 planes P_0 = lo, ...,
+// P_n = hi of the n = 2^D depth-D cells and a pad float, the scene's block
+// rounded up to 16 bytes. Launches whose scene table and planes would exceed
+// kPlaneLds bytes skip the planes.
+constexpr size_t kPlaneLds = 26624;
+__host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
+__host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) { return (4u + 3u * axis_stride(depth) + 3u) & ~3u; }
 
-// Split planes of one axis, nested midpoints computed with the descent's own
-// operations (kernel.cu:165-176), so cell boxes are the descent's boxes bit
-// for bit. Returns whether they support the direct cell lookup of
-// plane_cell: finite, each within 0.2 cell of the uniform grid, and an
-// accurate scale.
-__device__ bool make_planes(float lo, float hi, float* out) {
-    float pl[17];
+// Split planes of one axis for n = 2^D cells (pl[k] = P_k, then the pad) and
+// its scale, nested midpoints computed with the descent's own operations
+// (kernel.cu:165-176), so cell boxes are the descent's boxes bit for bit.
+// Returns whether they support the direct cell lookup of plane_cell: finite,
+// each within 0.2 cell of the uniform grid, and an accurate scale.
+__device__ bool make_planes(float lo, float hi, uint32_t n, float* pl, float& scale_out) {
     pl[0] = lo;
-    pl[16] = hi;
-    for (int step = 16; step > 1; step >>= 1)
-        for (int k = 0; k < 16; k += step) pl[k + step / 2] = (pl[k] + pl[k + step]) * 0.5f;
+    pl[n] = hi;
+    // once per workgroup: kept rolled (unrolled, it would crowd the registers
+    // of the whole kernel)
+#pragma unroll 1
+    for (uint32_t step = n; step > 1; step >>= 1)
+#pragma unroll 1
+        for (uint32_t k = 0; k < n; k += step) pl[k + step / 2] = (pl[k] + pl[k + step]) * 0.5f;
     const float w = hi - lo;
-    const float scale = 16.0f / w;
-    const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / 16.0;
+    const float scale = static_cast<float>(n) / w;
+    const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / n;
     bool ok = w > 0.0f && w <= 0x1p127f && scale > 0.0f && scale <= 0x1p127f && cw > 0.0 &&
               fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6;
-    for (int k = 0; k <= 16; ++k) {
+#pragma unroll 1
+    for (uint32_t k = 0; k <= n; ++k)
         ok = ok && fabs(static_cast<double>(pl[k]) - (static_cast<double>(lo) + k * cw)) <= 0.2 * cw;
-        out[k] = pl[k];
-    }
-    out[16 + 1] = scale;
+    scale_out = scale;
+    pl[n + 1] = 0.0f;
     return ok;
 }
 
-// Depth-4 cell of p along one axis from its planes, and the cell's bounds.
-// With planes within 0.2 cell of uniform, u = (p - P_0) * scale - 0.25 lies
-// within (j - 0.46, j + 0.96) for the cell j that holds p (P_j <= p < P_j+1,
-// or j = 15 at p = P_16), so trunc(u) is j - 1 or j (0 when u < 0, where j is
-// 0); one comparison with the next plane settles it.
-__device__ __forceinline__ uint32_t plane_cell(float p, const float* pl, float& lo, float& hi) {
-    const float u = __builtin_fmaf(p - pl[0], pl[16 + 1], -0.25f);
-    const uint32_t j0 = static_cast<uint32_t>(static_cast<int32_t>(u));
-    const float a = pl[j0], b = pl[j0 + 1], c = pl[j0 + 2];  // pl[17] is read (unused) at j0 = 15
-    const bool up = p >= b && j0 < 15u;
+// Depth-D cell of p along one axis from its planes (pl[k] = P_k, P_0 = lo)
+// and scale, and the cell's bounds. With planes within 0.2 cell of uniform,
+// u = (p - P_0) * scale - 0.25 lies within (j - 0.46, j + 0.96) for the cell j
+// that holds p (P_j <= p < P_j+1, or j = n - 1 at p = P_n), so trunc(u) is
+// j - 1 or j (0 when u < 0, where j is 0); capped at n - 2 it is still j - 1
+// or j, and one comparison with the next plane settles it.
+__device__ __forceinline__ uint32_t plane_cell(float p, float lo0, float scale, const float* pl, uint32_t n, float& lo,
+                                               float& hi) {
+    const float u = __builtin_fmaf(p - lo0, scale, -0.25f);
+    const uint32_t j0 = min(static_cast<uint32_t>(static_cast<int32_t>(u)), n - 2u);
+    const float a = pl[j0], b = pl[j0 + 1], c = pl[j0 + 2];
+    const bool up = p >= b;
     lo = up ? b : a;
     hi = up ? c : b;
     return j0 + (up ? 1u : 0u);
 }
 
-template <bool kPlanes, bool kPoses>
+// kDepth > 0: the cell-table depth, with the scenes' split planes staged in
+// LDS; kDepth = 0: the depth is P.cell_depth and cells come from splits.
+template <int kDepth, bool kPoses>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
+    constexpr bool kPlanes = kDepth > 0;
     extern __shared__ SceneLds lds_scenes[];
     float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
     // `tame`: every scene box has coordinates below 2^100 in magnitude, so
@@ -215,13 +228,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     }
     tame = __syncthreads_and(tame);
     shallow = __syncthreads_and(shallow);
-    // `planes`: every scene's depth-4 cells can be located from its planes
+    // `planes`: every scene's depth-D cells can be located from its planes
     int planes = kPlanes ? 1 : 0;
+    const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
+    constexpr uint32_t kAxis = kPlanes ? axis_stride(kDepth) : 0u;    // floats per axis
+    constexpr uint32_t kScene = kPlanes ? scene_stride(kDepth) : 0u;  // floats per scene
+    constexpr uint32_t kCells = kPlanes ? (1u << kDepth) : 0u;        // cells per axis
     if (kPlanes) {
         for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
             const navi_relaid_scene& d = P.scenes[i / 3];
             const int a = i % 3;
-            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], lds_planes + i * kPlaneStride) ? 1 : 0;
+            float* hdr = lds_planes + (i / 3) * kScene;
+            float scale = 0.0f;
+            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], kCells, hdr + 4 + a * kAxis, scale) ? 1 : 0;
+            hdr[a] = scale;
+            if (a == 0) hdr[3] = 0.0f;
         }
         planes = __syncthreads_and(planes);
     }
@@ -244,7 +265,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     int32_t sem = 0, step = 0;
     uint32_t scene = 0;  // this ray's scene (an index into lds_scenes)
     Box lf{}, vd{}, pre{};
-    uint32_t lf_slot = 0, pre_rec = 0;
+    uint32_t lf_slot = 0;
+    uint32_t pre_cell = 0;  // the prefix cell's depth-4 indices x | y << 4 | z << 8 (split path)
     bool lf_ok = false, vd_ok = false, pre_ok = false;
 
     while (true) {
@@ -366,32 +388,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         const bool hit_lf = !hit_vd && !outside && lf_ok && in_box(px, py, pz, lf);
         const bool use_pre = pre_ok && in_box(px, py, pz, pre);
         bool descending = has_ray && !(hit_vd || outside || hit_lf);
-        Box cur;
-        cur.x0 = use_pre ? pre.x0 : dom.x0;
-        cur.y0 = use_pre ? pre.y0 : dom.y0;
-        cur.z0 = use_pre ? pre.z0 : dom.z0;
-        cur.x1 = use_pre ? pre.x1 : dom.x1;
-        cur.y1 = use_pre ? pre.y1 : dom.y1;
-        cur.z1 = use_pre ? pre.z1 : dom.z1;
-        uint32_t cur_rec = pre_rec;
+        Box cur = dom;
+        uint32_t cur_rec = 0;
         int32_t depth = kPrefixDepth;
         uint32_t slot = 0;
 
-        // ---- a descent from the root: locate the depth-4 cell, one root-table read ----
-        // The root table holds what four record reads from the root would
-        // meet (navi_build_root_table). The cell comes from the split planes
-        // when the scenes allow it, else from four splits done here; either
-        // way its box is the descent's box bit for bit.
-        if (descending && !use_pre) {
+        // ---- every descent: locate the depth-D cell, one cell-table read ----
+        // The cell table holds what D record reads from the root would meet
+        // (navi_build_cell_table). A fresh descent (kernel.cu:133-135) meets
+        // the cell that holds p by the >= rule of kernel.cu:165-176. A
+        // descent from the cached prefix cell (:120-132) meets the same cell,
+        // except on the prefix cell's upper faces, which the inclusive cache
+        // test admits: there it meets the cell's last sub-cell, one below the
+        // cell past the face. The cell comes from the split planes when the
+        // scenes allow it, else from splits done here; either way its box is
+        // the descent's box bit for bit.
+        if (descending) {
+            // the scene's scales and planes of x, y, z
+            const float* hdr = lds_planes + __umul24(scene, kScene);
+            const float* plx = hdr + 4;
+            const float* ply = plx + kAxis;
+            const float* plz = ply + kAxis;
             uint32_t jx = 0, jy = 0, jz = 0;
-            const float* pl = lds_planes + scene * (3 * kPlaneStride);
             if (kPlanes && planes) {
-                jx = plane_cell(px, pl, cur.x0, cur.x1);
-                jy = plane_cell(py, pl + kPlaneStride, cur.y0, cur.y1);
-                jz = plane_cell(pz, pl + 2 * kPlaneStride, cur.z0, cur.z1);
+                const float4 scale = *reinterpret_cast<const float4*>(hdr);
+                jx = plane_cell(px, dom.x0, scale.x, plx, kCells, cur.x0, cur.x1);
+                jy = plane_cell(py, dom.y0, scale.y, ply, kCells, cur.y0, cur.y1);
+                jz = plane_cell(pz, dom.z0, scale.z, plz, kCells, cur.z0, cur.z1);
+                // p lies in the prefix cell, so only its upper faces can put the
+                // looked-up cell outside it
+                if (use_pre && !(px < pre.x1 && py < pre.y1 && pz < pre.z1)) {  // rare
+                    const bool fx = px == pre.x1 && cur.x0 == px;
+                    const bool fy = py == pre.y1 && cur.y0 == py;
+                    const bool fz = pz == pre.z1 && cur.z0 == pz;
+                    jx -= fx ? 1u : 0u;
+                    jy -= fy ? 1u : 0u;
+                    jz -= fz ? 1u : 0u;
+                    const float lx = plx[jx], ly = ply[jy], lz = plz[jz];
+                    cur.x1 = fx ? cur.x0 : cur.x1;
+                    cur.y1 = fy ? cur.y0 : cur.y1;
+                    cur.z1 = fz ? cur.z0 : cur.z1;
+                    cur.x0 = fx ? lx : cur.x0;
+                    cur.y0 = fy ? ly : cur.y0;
+                    cur.z0 = fz ? lz : cur.z0;
+                }
             } else {
+                // a prefix descent starts from the cached cell, a fresh one
+                // from the domain, four levels up
+                cur.x0 = use_pre ? pre.x0 : dom.x0;
+                cur.y0 = use_pre ? pre.y0 : dom.y0;
+                cur.z0 = use_pre ? pre.z0 : dom.z0;
+                cur.x1 = use_pre ? pre.x1 : dom.x1;
+                cur.y1 = use_pre ? pre.y1 : dom.y1;
+                cur.z1 = use_pre ? pre.z1 : dom.z1;
+                jx = use_pre ? (pre_cell & 15u) : 0u;
+                jy = use_pre ? ((pre_cell >> 4) & 15u) : 0u;
+                jz = use_pre ? (pre_cell >> 8) : 0u;
 #pragma unroll
-                for (int l = 0; l < kPrefixDepth; ++l) {
+                for (int l = 0; l < kPrefixDepth; ++l) {  // fresh lanes only
+                    const float mx = (cur.x0 + cur.x1) * 0.5f;
+                    const float my = (cur.y0 + cur.y1) * 0.5f;
+                    const float mz = (cur.z0 + cur.z1) * 0.5f;
+                    const bool gx = px >= mx, gy = py >= my, gz = pz >= mz;
+                    const bool sx = !use_pre, ux = sx && gx, uy = sx && gy, uz = sx && gz;
+                    cur.x0 = ux ? mx : cur.x0;
+                    cur.x1 = (sx && !gx) ? mx : cur.x1;
+                    cur.y0 = uy ? my : cur.y0;
+                    cur.y1 = (sx && !gy) ? my : cur.y1;
+                    cur.z0 = uz ? mz : cur.z0;
+                    cur.z1 = (sx && !gz) ? mz : cur.z1;
+                    jx = sx ? append_bit(jx, gx) : jx;
+                    jy = sx ? append_bit(jy, gy) : jy;
+                    jz = sx ? append_bit(jz, gz) : jz;
+                }
+#pragma unroll 1
+                for (uint32_t l = kPrefixDepth; l < D; ++l) {
                     const float mx = (cur.x0 + cur.x1) * 0.5f;
                     const float my = (cur.y0 + cur.y1) * 0.5f;
                     const float mz = (cur.z0 + cur.z1) * 0.5f;
@@ -407,40 +478,52 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     jz = append_bit(jz, gz);
                 }
             }
-            const uint64_t e = P.root_table[(((scene << 4 | jz) << 4 | jy) << 4) | jx];
+            const uint64_t e = P.root_table[(((scene << D | jz) << D | jy) << D) | jx];
             slot = static_cast<uint32_t>(e);
             depth = static_cast<int32_t>(e >> 32);
-            if (depth < kPrefixDepth) {
-                // leaf / void / fault above depth 4 (rare): its box is the one
-                // after `depth` splits
+            if (depth < static_cast<int32_t>(D)) {
+                // leaf / void / fault above depth D: its box is the one after
+                // `depth` splits
                 if (kPlanes && planes) {
-                    const uint32_t sh = static_cast<uint32_t>(kPrefixDepth - depth);
+                    const uint32_t sh = D - static_cast<uint32_t>(depth);
                     const uint32_t w = 1u << sh;
                     const uint32_t kx = (jx >> sh) << sh, ky = (jy >> sh) << sh, kz = (jz >> sh) << sh;
-                    cur = Box{pl[kx], pl[kPlaneStride + ky], pl[2 * kPlaneStride + kz],
-                              pl[kx + w], pl[kPlaneStride + ky + w], pl[2 * kPlaneStride + kz + w]};
+                    cur = Box{plx[kx], ply[ky], plz[kz], plx[kx + w], ply[ky + w], plz[kz + w]};
                 } else {
                     cur = dom;
+#pragma unroll 1
                     for (int32_t l = 0; l < depth; ++l) {
-                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        const uint32_t b = D - 1u - static_cast<uint32_t>(l);
                         split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
                     }
                 }
             }
-            const bool internal = slot < kSlotBadChild;  // an internal node at depth 4
-            pre.x0 = internal ? cur.x0 : pre.x0;      // kernel.cu:154-163
-            pre.y0 = internal ? cur.y0 : pre.y0;
-            pre.z0 = internal ? cur.z0 : pre.z0;
-            pre.x1 = internal ? cur.x1 : pre.x1;
-            pre.y1 = internal ? cur.y1 : pre.y1;
-            pre.z1 = internal ? cur.z1 : pre.z1;
-            pre_rec = internal ? slot : pre_rec;
-            pre_ok = pre_ok || internal;
+            // kernel.cu:154-163: a fresh descent caches the depth-4 node when it
+            // is internal, i.e. when the path goes below depth 4; the cell is
+            // the depth-4 ancestor of the depth-D cell
+            const bool save = !use_pre && (depth > kPrefixDepth || (depth == kPrefixDepth && slot < kSlotBadChild));
+            if (save) {
+                const uint32_t sh = D - kPrefixDepth;
+                const uint32_t kx = jx >> sh, ky = jy >> sh, kz = jz >> sh;
+                if (kPlanes && planes) {
+                    const uint32_t w = 1u << sh;
+                    const uint32_t ax = kx << sh, ay = ky << sh, az = kz << sh;
+                    pre = Box{plx[ax], ply[ay], plz[az], plx[ax + w], ply[ay + w], plz[az + w]};
+                } else {
+                    pre = dom;
+                    for (int l = 0; l < kPrefixDepth; ++l) {
+                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        split_box(pre, ((kx >> b) & 1u) | (((ky >> b) & 1u) << 1) | (((kz >> b) & 1u) << 2));
+                    }
+                }
+                if (!(kPlanes && planes)) pre_cell = kx | (ky << 4) | (kz << 8);
+                pre_ok = true;
+            }
             cur_rec = slot;
-            descending = internal;
+            descending = slot < kSlotBadChild;  // an internal node at depth D
         }
 
-        // ---- descend below depth 4, one 4-byte gather per level (kernel.cu:136-199) ----
+        // ---- descend below depth D, one 4-byte gather per level (kernel.cu:136-199) ----
         // A per-lane loop: lanes that found their leaf / void leave it and are
         // masked off; the wave runs it as long as its deepest descent.
         // Child slots from navi_relayout are always in range; the clamp only
@@ -466,9 +549,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // ---- classify the query result and update the caches ----
         // Lanes that did not descend keep slot == 0 (an internal slot), so the
         // descent outcomes below are false for them. (The shallow loop leaves
-        // `depth` at the table's value, <= 4: below the limit, as every slot of
-        // a shallow scene is. Shallow scenes carry no bad-child slots:
-        // navi_relayout and the root table turn them into faults, which they
+        // `depth` at the table's value, <= D <= 7: below the limit, as every
+        // slot of a shallow scene is. Shallow scenes carry no bad-child slots:
+        // navi_relayout and the cell table turn them into faults, which they
         // are at every depth < 32.)
         const bool new_leaf = (slot & 0x80000000u) != 0u && depth < kMaxDepth;  // examined at depth < 32
         const bool new_void = slot == kSlotVoid;
@@ -620,13 +703,20 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.unit_rays = kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
-    const bool use_planes = P.n_scenes <= kPlaneScenes;
-    const size_t lds = static_cast<size_t>(P.n_scenes) *
-                       (sizeof(SceneLds) + (use_planes ? 3 * kPlaneStride * sizeof(float) : 0));
+    const size_t plane_bytes = static_cast<size_t>(scene_stride(P.cell_depth)) * sizeof(float);
+    const bool use_planes = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + plane_bytes) <= kPlaneLds;
+    const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (use_planes ? plane_bytes : 0));
     const bool poses = P.local_dirs != nullptr;
-    const auto kernel = use_planes ? (poses ? trace_relaid_kernel<true, true> : trace_relaid_kernel<true, false>)
-                                   : (poses ? trace_relaid_kernel<false, true> : trace_relaid_kernel<false, false>);
-    const auto key = std::make_pair(2 * static_cast<int>(use_planes) + static_cast<int>(poses), lds);
+    const int depth = use_planes ? static_cast<int>(P.cell_depth) : 0;
+    void (*kernel)(RelaidParams) = nullptr;
+    switch (depth) {
+        case 4: kernel = poses ? trace_relaid_kernel<4, true> : trace_relaid_kernel<4, false>; break;
+        case 5: kernel = poses ? trace_relaid_kernel<5, true> : trace_relaid_kernel<5, false>; break;
+        case 6: kernel = poses ? trace_relaid_kernel<6, true> : trace_relaid_kernel<6, false>; break;
+        case 7: kernel = poses ? trace_relaid_kernel<7, true> : trace_relaid_kernel<7, false>; break;
+        default: kernel = poses ? trace_relaid_kernel<0, true> : trace_relaid_kernel<0, false>; break;
+    }
+    const auto key = std::make_pair(2 * depth + static_cast<int>(poses), lds);
     int grid_blocks = 0;
     {
         std::lock_guard<std::mutex> lock(g_queue_mu);
@@ -664,7 +754,7 @@ namespace navi {
 
 // Arguments shared by the two relaid entry points.
 int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                 int32_t n_scenes, const uint64_t* root_tables, const int32_t* env_scene,
+                 int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth, const int32_t* env_scene,
                  const int32_t* env_order, int64_t n_envs, int64_t rays_per_env, int32_t elevation_bins,
                  float* out_distances, int32_t* out_semantics, int32_t max_steps, float max_distance,
                  float hit_epsilon, int32_t* out_steps) {
@@ -674,7 +764,8 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
     if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
-    if (!root_tables) return set_error(NAVI_E_ARG, "root_tables is required (navi_build_root_table)");
+    if (!root_tables) return set_error(NAVI_E_ARG, "root_tables is required (navi_build_cell_table)");
+    if (table_depth < 4 || table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
     // 32-bit slot addressing: record * 8 + octant must fit in uint32
     if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
@@ -690,6 +781,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     P.scenes = scenes;
     P.n_scenes = n_scenes;
     P.root_table = root_tables;
+    P.cell_depth = static_cast<uint32_t>(table_depth);
     P.env_scene = env_scene;
     P.env_order = env_order;
     P.n_rays = static_cast<uint32_t>(n_rays);
@@ -712,7 +804,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
 }  // namespace navi
 
 extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                                 int32_t n_scenes, const uint64_t* root_tables,
+                                 int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
                                  const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                                  int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                                  const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -720,9 +812,9 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
                                  int32_t* out_steps, void* stream) {
     using namespace navi;
     RelaidParams P;
-    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, env_scene, env_order, n_envs,
-                                  rays_per_env, elevation_bins, out_distances, out_semantics, max_steps,
-                                  max_distance, hit_epsilon, out_steps);
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, table_depth, env_scene,
+                                  env_order, n_envs, rays_per_env, elevation_bins, out_distances, out_semantics,
+                                  max_steps, max_distance, hit_epsilon, out_steps);
     if (code != NAVI_OK || P.n_rays == 0) return code;
     if (!origins || !dirs) return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
     P.origins = origins;
@@ -732,7 +824,8 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
 
 extern "C" int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records,
                                        const navi_relaid_scene* scenes, int32_t n_scenes,
-                                       const uint64_t* root_tables, const int32_t* env_scene,
+                                       const uint64_t* root_tables, int32_t table_depth,
+                                       const int32_t* env_scene,
                                        const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
                                        int32_t elevation_bins, const float* local_dirs, const float* env_pos,
                                        const float* env_rot, float* out_distances, int32_t* out_semantics,
@@ -740,9 +833,9 @@ extern "C" int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_recor
                                        int32_t* out_steps, void* stream) {
     using namespace navi;
     RelaidParams P;
-    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, env_scene, env_order, n_envs,
-                                  rays_per_env, elevation_bins, out_distances, out_semantics, max_steps,
-                                  max_distance, hit_epsilon, out_steps);
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, table_depth, env_scene,
+                                  env_order, n_envs, rays_per_env, elevation_bins, out_distances, out_semantics,
+                                  max_steps, max_distance, hit_epsilon, out_steps);
     if (code != NAVI_OK || P.n_rays == 0) return code;
     if (!local_dirs || !env_pos || !env_rot)
         return set_error(NAVI_E_ARG, "local_dirs, env_pos and env_rot must be non-null");

@@ -20,6 +20,25 @@ import torch
 from . import _native
 
 
+# The tracer stages each scene's split planes in LDS when the scene table and
+# planes of a launch fit in this many bytes (kPlaneLds in trace_relaid.hip):
+# 32 bytes per scene plus scene_stride(D) floats.
+PLANE_LDS_BYTES = 26624
+
+
+def _plane_bytes(depth: int) -> int:
+    return 4 * ((4 + 3 * ((1 << depth) + 2) + 3) & ~3)
+
+
+def default_table_depth(n_scenes: int) -> int:
+    """The deepest cell table (at most 6: 2 MiB per scene) whose split planes still fit
+    the tracer's LDS budget for ``n_scenes`` scenes; 4 when none does."""
+    for depth in (6, 5):
+        if n_scenes * (32 + _plane_bytes(depth)) <= PLANE_LDS_BYTES:
+            return depth
+    return 4
+
+
 class ResidentScenes:
     """Concatenated word pool + scene table on one device.
 
@@ -29,9 +48,12 @@ class ResidentScenes:
     """
 
     def __init__(self, scenes: Sequence[tuple[np.ndarray, Sequence[float], Sequence[float]]],
-                 device: str | torch.device = "cuda", *, keep_words: bool = True) -> None:
+                 device: str | torch.device = "cuda", *, keep_words: bool = True,
+                 table_depth: int | None = None) -> None:
         if not scenes:
             raise ValueError("at least one scene is required")
+        if table_depth is not None and not 4 <= int(table_depth) <= 7:
+            raise ValueError("table_depth must be in [4, 7]")
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
@@ -85,7 +107,8 @@ class ResidentScenes:
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
-            tables = np.concatenate([_native.root_table(allrec[:roff], int(rtable[i]["root_slot"]))
+            self.table_depth = int(table_depth) if table_depth is not None else default_table_depth(len(scenes))
+            tables = np.concatenate([_native.cell_table(allrec[:roff], int(rtable[i]["root_slot"]), self.table_depth)
                                      for i in range(len(scenes))])
             for i in range(len(scenes)):
                 rtable[i]["max_depth"] = _native.record_depth(allrec[:roff], int(rtable[i]["root_slot"]))
@@ -147,7 +170,7 @@ class ResidentScenes:
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 code = _native.lib().navi_trace_relaid(
                     self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                    self.root_tables.data_ptr(),
+                    self.root_tables.data_ptr(), self.table_depth,
                     env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
                     int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
                     out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),
@@ -207,7 +230,8 @@ class ResidentScenes:
             stream = torch.cuda.current_stream(self.device).cuda_stream
             code = _native.lib().navi_trace_relaid_poses(
                 self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                self.root_tables.data_ptr(), ptrs[0], order.data_ptr() if order is not None else None, e, r,
+                self.root_tables.data_ptr(), self.table_depth, ptrs[0],
+                order.data_ptr() if order is not None else None, e, r,
                 int(elevation_bins or 0), ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], int(max_steps),
                 float(max_distance), float(hit_epsilon), ptrs[6], stream)
         _native.check(code)
@@ -218,6 +242,7 @@ class ResidentScenes:
         q = _native.PointQueries()
         q.records, q.n_records = self.records.data_ptr(), self.n_records
         q.scenes, q.n_scenes, q.root_tables = self.relaid_table.data_ptr(), self.n_scenes, self.root_tables.data_ptr()
+        q.table_depth = self.table_depth
         q.points = self._check("points", points, torch.float32, (p, 3))
         q.n_points = p
         q.point_scene = self._check(prefix + "point_scene", point_scene, torch.int32, (p,), optional=True)

@@ -17,7 +17,7 @@ traced in angular tiles) and ``kernel``.
 
 Kernels. ``kernel="auto"`` (default) traces with the record-layout tracer
 (``navi_trace_relaid``): the first call with a given DAG tensor copies its words
-to the host once, converts them (``navi_relayout``, ``navi_build_root_table``)
+to the host once, converts them (``navi_relayout``, ``navi_build_cell_table``)
 and keeps the device copy, keyed by the tensor object, its version counter
 (in-place writes invalidate it) and the bbox. DAGs the record layout cannot
 hold (a leaf semantic above 0x7fff) and batches above 2^30 rays use the
@@ -200,7 +200,7 @@ def cast_rays(
             stream = torch.cuda.current_stream(dev).cuda_stream
             code = _native.lib().navi_trace_relaid(
                 scenes.records.data_ptr(), scenes.n_records, scenes.relaid_table.data_ptr(), 1,
-                scenes.root_tables.data_ptr(), None, None, n_envs, rays, int(elevation_bins),
+                scenes.root_tables.data_ptr(), scenes.table_depth, None, None, n_envs, rays, int(elevation_bins),
                 origins.data_ptr(), dirs.data_ptr(), out_distances.data_ptr(), out_semantics.data_ptr(),
                 int(max_steps), float(max_distance), float(hit_epsilon),
                 out_steps.data_ptr() if out_steps is not None else None, stream,

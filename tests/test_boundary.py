@@ -6,6 +6,7 @@ and its host-side argument checks. No GPU kernel is launched here.
 
 from __future__ import annotations
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -131,8 +132,6 @@ def _declared_functions():
 
 
 def test_every_declared_symbol_is_exported():
-    import ctypes
-
     declared = _declared_functions()
     assert "navi_cast_rays" in declared and "navi_trace_relaid" in declared
     libs = [ctypes.CDLL(str(ROOT / "navi_amd" / "_lib" / n)) for n in ("libnavi_trace.so", "libnavi_scene.so")]
@@ -153,11 +152,19 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     code = lib.navi_cast_rays(1, 1, None, None, None, None, 0, 4, 1.0, f3([0, 0, 0]), f3([1, 1, 1]), 1, 0.01,
                               None, None, None)
     assert code == _native.NAVI_OK  # empty batch: no launch
-    code = lib.navi_trace_relaid(1, 1, 1, 1, 1, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01,
+    code = lib.navi_trace_relaid(1, 1, 1, 1, 1, 6, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01,
                                   None, None)
     assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
-    code = lib.navi_trace_relaid(1, 1, 1, 1, None, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
+    code = lib.navi_trace_relaid(1, 1, 1, 1, None, 6, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
     assert code == _native.NAVI_E_ARG and "root_tables" in _native.last_error()
+    for depth in (3, 8):
+        code = lib.navi_trace_relaid(1, 1, 1, 1, 1, depth, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None,
+                                      None)
+        assert code == _native.NAVI_E_ARG and "table_depth" in _native.last_error()
+    q = _native.PointQueries(records=1, n_records=1, scenes=1, n_scenes=1, root_tables=1, table_depth=3,
+                             points=1, n_points=1, out_distances=1, out_semantics=1)
+    assert lib.navi_point_query(ctypes.byref(q), None) == _native.NAVI_E_ARG
+    assert "table_depth" in _native.last_error()
 
 
 def test_relayout_on_the_host():
@@ -193,18 +200,20 @@ def test_relayout_on_the_host():
         _native.relayout(np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], np.uint64))
 
 
-def _walk(rec, root, cell):
-    """Four levels of record reads from the root along the octants of `cell`."""
+def _walk(rec, root, cell, depth=4):
+    """`depth` levels of record reads from the root along the octants of `cell`
+    (x bits low, then y, then z, `depth` bits each)."""
     if root >> 31:
         return root, 0
     r = root
-    ix, iy, iz = cell & 15, (cell >> 4) & 15, cell >> 8
-    for lvl in range(4):
-        b = 3 - lvl
+    m = (1 << depth) - 1
+    ix, iy, iz = cell & m, (cell >> depth) & m, cell >> (2 * depth)
+    for lvl in range(depth):
+        b = depth - 1 - lvl
         oct_ = ((ix >> b) & 1) | ((iy >> b) & 1) << 1 | ((iz >> b) & 1) << 2
         slot = int(rec[r][oct_]) if r < rec.shape[0] else 0x7FFFFFFE
-        if slot >= 0x7FFFFFFD or lvl == 3:
-            return slot, lvl + 1
+        if slot >= 0x7FFFFFFD or lvl == depth - 1:
+            return (0x7FFFFFFE if slot == 0x7FFFFFFD else slot), lvl + 1
         r = slot
 
 
@@ -237,6 +246,30 @@ def test_root_table_matches_record_walks(case):
         assert set(depths.tolist()) == {0} and set(slots.tolist()) == {root}
     if case in ("room", "offset"):
         assert (depths == 4).any() and (slots[depths == 4] < 0x7FFFFFFD).any()
+
+
+@pytest.mark.parametrize("depth", [4, 5, 6, 7])
+def test_cell_table_matches_record_walks(depth):
+    """navi_build_cell_table at every depth against record walks (every cell up to
+    depth 5, a seeded sample deeper), on a scene whose leaves lie at depths 5 to 7,
+    with a pool offset; at depth 4 it equals navi_build_root_table."""
+    from navi_amd import scenes as S
+
+    rec, root, _ = _native.relayout(S.box_room(resolution=128, seed=3).compile())
+    rec = np.concatenate([np.full((5, 8), 0x7FFFFFFF, np.uint32), np.where(rec < 0x7FFFFFFD, rec + 5, rec)])
+    root += 5
+    table = _native.cell_table(rec, root, depth)
+    assert table.size == 8 ** depth
+    if depth == 4:
+        assert np.array_equal(table, _native.root_table(rec, root))
+    cells = range(table.size) if depth <= 5 else np.random.default_rng(depth).integers(0, table.size, 20000)
+    for cell in cells:
+        slot, d = _walk(rec, root, int(cell), depth)
+        assert (int(table[cell] & 0xFFFFFFFF), int(table[cell] >> 32)) == (slot, d), cell
+    depths = table >> 32
+    assert (depths == depth).any() and (depths < depth).any()
+    with pytest.raises(RuntimeError, match="table depth"):
+        _native.cell_table(rec, root, 8)
 
 
 def _longest_chain(rec, root):

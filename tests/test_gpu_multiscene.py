@@ -262,15 +262,16 @@ def test_relaid_descent_limit_chains(gpu, corpus):
 
 
 def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
-    """70 resident scenes (more than the launch keeps split planes for in LDS),
+    """100 resident scenes (more than the launch keeps split planes for in LDS),
     and domains too narrow for their magnitude (float split planes collapse),
     both located by in-register splits instead of the plane lookup."""
-    from navi_amd.multiscene import ResidentScenes
+    from navi_amd.multiscene import PLANE_LDS_BYTES, ResidentScenes, _plane_bytes
 
-    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(70)]
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(100)]
     res = ResidentScenes(many)
+    assert res.table_depth == 4 and 100 * (32 + _plane_bytes(4)) > PLANE_LDS_BYTES
     env_scene, o, d = _rays(corpus, 24, 16, 16, seed=31)
-    env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 70
+    env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 100
     ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 128, 30.0)
     _compare(_run(res, env_scene, o, d, 128, 30.0, elevation_bins=16), ref, 30.0, "many")
 
@@ -286,6 +287,57 @@ def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
     d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
     ref = _oracle_multi([words] * 2, narrow, env_scene, o, d, 64, 5.0)
     _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, "narrow")
+
+
+@pytest.mark.parametrize("depth", [4, 5, 6, 7])
+def test_relaid_every_table_depth(gpu, corpus, depth):
+    """Descents start at the cell table's depth (4 to 7): the cell from the LDS
+    split planes, and for domains too narrow for their planes from splits in
+    registers. Canonical and random rays, inside and outside the domains,
+    against the oracle."""
+    from navi_amd.multiscene import ResidentScenes
+
+    scenes = [(c.words, c.bbox_min_list, c.bbox_max) for c in corpus]
+    bounds = [c.bbox_min_list + c.bbox_max for c in corpus]
+    res = ResidentScenes(scenes, table_depth=depth)
+    assert res.table_depth == depth
+    env_scene, o, d = _rays(corpus, 16, 32, 16, seed=40 + depth)
+    ref = _oracle_multi([c.words for c in corpus], bounds, env_scene, o, d, 256, 30.0)
+    _compare(_run(res, env_scene, o, d, 256, 30.0, elevation_bins=16), ref, 30.0, f"depth{depth}")
+    rng = np.random.default_rng(depth)
+    lo = np.array([bounds[s][:3] for s in env_scene]) - 2.0
+    hi = np.array([bounds[s][3:] for s in env_scene]) + 2.0
+    o = rng.uniform(lo[:, None, :], hi[:, None, :], (16, 512, 3)).astype(np.float32)
+    d = rng.normal(size=(16, 512, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    ref = _oracle_multi([c.words for c in corpus], bounds, env_scene, o, d, 300, 45.0)
+    _compare(_run(res, env_scene, o, d, 300, 45.0), ref, 45.0, f"depth{depth}/random")
+
+    words = corpus[0].words
+    narrow = [[1000.0, -2.0, 5.0, 1000.00048828125, 2.0, 5.0000019073486328], [-1.0, -1.0, -1.0, 1.0, 1.0, 1.0]]
+    res = ResidentScenes([(words, b[:3], b[3:]) for b in narrow], table_depth=depth)
+    env_scene = np.array([0, 1, 0], np.int32)
+    b = np.array(narrow, np.float64)[env_scene]
+    o = rng.uniform(b[:, None, :3], b[:, None, 3:], (3, 400, 3)).astype(np.float32)
+    d = rng.normal(size=(3, 400, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    ref = _oracle_multi([words] * 2, narrow, env_scene, o, d, 64, 5.0)
+    _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, f"depth{depth}/narrow")
+
+
+@pytest.mark.parametrize("depth", [5, 6])
+def test_relaid_deep_tables_without_planes(gpu, corpus, depth):
+    """60 resident scenes with cell tables deeper than 4: more split planes than
+    the launch stages in LDS, so every cell comes from splits in registers."""
+    from navi_amd.multiscene import PLANE_LDS_BYTES, ResidentScenes, _plane_bytes
+
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(60)]
+    assert 60 * (32 + _plane_bytes(depth)) > PLANE_LDS_BYTES
+    res = ResidentScenes(many, table_depth=depth)
+    env_scene, o, d = _rays(corpus, 20, 16, 16, seed=50 + depth)
+    env_scene = (env_scene + 4 * np.arange(20, dtype=np.int32)) % 60
+    ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 200, 30.0)
+    _compare(_run(res, env_scene, o, d, 200, 30.0, elevation_bins=16), ref, 30.0, f"noplanes{depth}")
 
 
 @pytest.mark.parametrize("n", [31, 32])
@@ -350,7 +402,7 @@ def test_relaid_env_order_entries_out_of_range_are_skipped(gpu, corpus):
     out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
     code = _native.lib().navi_trace_relaid(
         res.records.data_ptr(), res.n_records, res.relaid_table.data_ptr(), res.n_scenes,
-        res.root_tables.data_ptr(), t_es.data_ptr(), order.data_ptr(), 6, 16 * 8, 8, t_o.data_ptr(),
+        res.root_tables.data_ptr(), res.table_depth, t_es.data_ptr(), order.data_ptr(), 6, 16 * 8, 8, t_o.data_ptr(),
         t_d.data_ptr(), out_d.data_ptr(), out_s.data_ptr(), 64, 30.0, 0.01, None,
         torch.cuda.current_stream().cuda_stream)
     _native.check(code)

@@ -118,7 +118,8 @@ def _same_bits(a, b):
         np.where(np.isnan(b), np.float32(np.nan), b).view(np.uint32))
 
 
-def test_point_queries(gpu, corpus):
+@pytest.mark.parametrize("depth", [None, 4, 7])
+def test_point_queries(gpu, corpus, depth):
     import torch
 
     from tests.test_boundary import _chain_words
@@ -131,7 +132,7 @@ def test_point_queries(gpu, corpus):
     scenes += [(chain, [0, 0, 0], [1, 1, 1]), (bad, [0, 0, 0], [1, 1, 1]), (leaf, [-1, -1, -1], [1, 1, 1])]
     from navi_amd.multiscene import ResidentScenes
 
-    res = ResidentScenes(scenes)
+    res = ResidentScenes(scenes, table_depth=depth)
     bounds = [list(s[1]) + list(s[2]) for s in scenes]
     scene, pts = _point_cases(corpus, 3000, seed=12)
     extra = np.array([[1, 1, 1], [0.999, 0.999, 0.999], [0.3, 0.2, 0.9]], np.float32)
