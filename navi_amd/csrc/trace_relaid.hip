@@ -13,12 +13,12 @@
 //     take the next rays (ballot + mbcnt rank), so a wave never idles on a few
 //     long rays;
 //   * one march step per outer iteration for every lane: the void / domain /
-//     leaf / prefix tests; a descent from the root locates its depth-4 cell
-//     (split planes staged in LDS, or four splits) and reads one root-table
-//     entry; then a per-lane loop reads one 4-byte slot per level until every
-//     lane of the wave has its leaf / void cell; then the step resolves with
-//     selects, and lanes whose step was a leaf take up to two more steps that
-//     the leaf cache answers alone;
+//     leaf / prefix tests; a descent, from the root or the cached prefix
+//     cell, locates its depth-D cell (split planes staged in LDS, or splits)
+//     and reads one cell-table entry; then a per-lane loop reads one 4-byte
+//     slot per level until every lane of the wave has its leaf / void cell;
+//     then the step resolves with selects, and lanes whose step was a leaf
+//     take one more step if the leaf cache answers it alone;
 //   * work order: envs in the order given (callers sort them by scene so the
 //     resident scenes stream through L2 / MALL one or two at a time) and, when
 //     the elevation count is a multiple of 8, 8 x 8 (az x el) tiles of the
@@ -138,7 +138,7 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
 }
 
 constexpr uint32_t kRefillMin = 8;
-constexpr uint32_t kLeafRun = 2;  // leaf-cache steps taken after a leaf step
+constexpr uint32_t kLeafRun = 1;  // leaf-cache steps taken after a leaf step
 constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
 constexpr uint32_t kSmallUnitRays = 64;  // one tile, for small batches
 
@@ -231,9 +231,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     // `planes`: every scene's depth-D cells can be located from its planes
     int planes = kPlanes ? 1 : 0;
     const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
-    constexpr uint32_t kAxis = kPlanes ? axis_stride(kDepth) : 0u;    // floats per axis
-    constexpr uint32_t kScene = kPlanes ? scene_stride(kDepth) : 0u;  // floats per scene
-    constexpr uint32_t kCells = kPlanes ? (1u << kDepth) : 0u;        // cells per axis
+    // The planes go down to depth kPD = min(D, 6) (deeper ones would crowd LDS);
+    // a depth-7 cell is one split below its depth-6 cell.
+    constexpr uint32_t kPD = kPlanes ? (kDepth < 6 ? kDepth : 6) : 0u;
+    constexpr uint32_t kAxis = kPlanes ? axis_stride(kPD) : 0u;    // floats per axis
+    constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
+    constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
     if (kPlanes) {
         for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
             const navi_relaid_scene& d = P.scenes[i / 3];
@@ -432,6 +435,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     cur.y0 = fy ? ly : cur.y0;
                     cur.z0 = fz ? lz : cur.z0;
                 }
+#pragma unroll
+                for (int l = static_cast<int>(kPD); l < kDepth; ++l) {
+                    const float mx = (cur.x0 + cur.x1) * 0.5f;
+                    const float my = (cur.y0 + cur.y1) * 0.5f;
+                    const float mz = (cur.z0 + cur.z1) * 0.5f;
+                    const bool gx = px >= mx, gy = py >= my, gz = pz >= mz;
+                    cur.x0 = gx ? mx : cur.x0;
+                    cur.x1 = gx ? cur.x1 : mx;
+                    cur.y0 = gy ? my : cur.y0;
+                    cur.y1 = gy ? cur.y1 : my;
+                    cur.z0 = gz ? mz : cur.z0;
+                    cur.z1 = gz ? cur.z1 : mz;
+                    jx = append_bit(jx, gx);
+                    jy = append_bit(jy, gy);
+                    jz = append_bit(jz, gz);
+                }
             } else {
                 // a prefix descent starts from the cached cell, a fresh one
                 // from the domain, four levels up
@@ -484,10 +503,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             if (depth < static_cast<int32_t>(D)) {
                 // leaf / void / fault above depth D: its box is the one after
                 // `depth` splits
-                if (kPlanes && planes) {
+                if (kPlanes && planes) {  // depth < D <= 7, so depth <= kPD
                     const uint32_t sh = D - static_cast<uint32_t>(depth);
-                    const uint32_t w = 1u << sh;
-                    const uint32_t kx = (jx >> sh) << sh, ky = (jy >> sh) << sh, kz = (jz >> sh) << sh;
+                    const uint32_t up = kPD - static_cast<uint32_t>(depth);
+                    const uint32_t w = 1u << up;
+                    const uint32_t kx = (jx >> sh) << up, ky = (jy >> sh) << up, kz = (jz >> sh) << up;
                     cur = Box{plx[kx], ply[ky], plz[kz], plx[kx + w], ply[ky + w], plz[kz + w]};
                 } else {
                     cur = dom;
@@ -506,8 +526,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 const uint32_t sh = D - kPrefixDepth;
                 const uint32_t kx = jx >> sh, ky = jy >> sh, kz = jz >> sh;
                 if (kPlanes && planes) {
-                    const uint32_t w = 1u << sh;
-                    const uint32_t ax = kx << sh, ay = ky << sh, az = kz << sh;
+                    const uint32_t up = kPD - kPrefixDepth;
+                    const uint32_t w = 1u << up;
+                    const uint32_t ax = kx << up, ay = ky << up, az = kz << up;
                     pre = Box{plx[ax], ply[ay], plz[az], plx[ax + w], ply[ay + w], plz[az + w]};
                 } else {
                     pre = dom;
@@ -703,7 +724,7 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.unit_rays = kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
-    const size_t plane_bytes = static_cast<size_t>(scene_stride(P.cell_depth)) * sizeof(float);
+    const size_t plane_bytes = static_cast<size_t>(scene_stride(P.cell_depth < 6 ? P.cell_depth : 6)) * sizeof(float);
     const bool use_planes = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + plane_bytes) <= kPlaneLds;
     const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (use_planes ? plane_bytes : 0));
     const bool poses = P.local_dirs != nullptr;

@@ -27,14 +27,21 @@ PLANE_LDS_BYTES = 26624
 
 
 def _plane_bytes(depth: int) -> int:
+    depth = min(depth, 6)  # deeper cells are one split below their depth-6 cell
     return 4 * ((4 + 3 * ((1 << depth) + 2) + 3) & ~3)
 
 
+# Cell tables take 8 bytes per cell: 2 MiB per scene at depth 6, 16 MiB at 7.
+TABLE_BYTES_BUDGET = 256 << 20
+
+
 def default_table_depth(n_scenes: int) -> int:
-    """The deepest cell table (at most 6: 2 MiB per scene) whose split planes still fit
-    the tracer's LDS budget for ``n_scenes`` scenes; 4 when none does."""
-    for depth in (6, 5):
-        if n_scenes * (32 + _plane_bytes(depth)) <= PLANE_LDS_BYTES:
+    """The deepest cell table (at most 7) whose split planes fit the tracer's LDS budget
+    for ``n_scenes`` scenes and whose tables stay within ``TABLE_BYTES_BUDGET``; 4 when
+    none does (16 scenes: 7; up to 31: 6; up to 57: 5)."""
+    for depth in (7, 6, 5):
+        if (n_scenes * (32 + _plane_bytes(depth)) <= PLANE_LDS_BYTES
+                and n_scenes * 8 ** depth * 8 <= TABLE_BYTES_BUDGET):
             return depth
     return 4
 
@@ -107,11 +114,17 @@ class ResidentScenes:
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
-            self.table_depth = int(table_depth) if table_depth is not None else default_table_depth(len(scenes))
-            tables = np.concatenate([_native.cell_table(allrec[:roff], int(rtable[i]["root_slot"]), self.table_depth)
-                                     for i in range(len(scenes))])
             for i in range(len(scenes)):
                 rtable[i]["max_depth"] = _native.record_depth(allrec[:roff], int(rtable[i]["root_slot"]))
+            if table_depth is not None:
+                self.table_depth = int(table_depth)
+            else:
+                # no deeper than one level below the deepest record: such a table
+                # already answers every descent
+                deepest = max(int(d) for d in rtable["max_depth"])  # 0xffffffff for a cycle
+                self.table_depth = max(4, min(default_table_depth(len(scenes)), deepest + 1))
+            tables = np.concatenate([_native.cell_table(allrec[:roff], int(rtable[i]["root_slot"]), self.table_depth)
+                                     for i in range(len(scenes))])
             self.root_tables = torch.from_numpy(tables.view(np.int64)).to(self.device)
             self.n_records = int(roff)
             self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)
