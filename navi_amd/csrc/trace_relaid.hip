@@ -251,6 +251,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     }
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    // The record pool as a buffer resource: 32-bit byte offsets, and the
+    // hardware bounds every read by the pool's size (at most 2^27 records,
+    // 4 GiB). Dword 3 = 0x00020000: 32-bit data format, as gfx9 raw buffers need.
+    const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(P.records), static_cast<short>(0), static_cast<int>(P.n_records * 32u), 0x00020000);
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
     // Static schedule: this wave's chunks are wave, wave + n_waves, ...
     const uint32_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0u;
@@ -547,17 +552,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // ---- descend below depth D, one 4-byte gather per level (kernel.cu:136-199) ----
         // A per-lane loop: lanes that found their leaf / void leave it and are
         // masked off; the wave runs it as long as its deepest descent.
-        // Child slots from navi_relayout are always in range; the clamp only
-        // keeps a corrupt caller-built pool inside its allocation.
+        // Child slots from navi_relayout are always in range; the buffer
+        // resource's bound only keeps a corrupt caller-built pool inside its
+        // allocation (a read past it returns 0).
         if (shallow) {
             while (descending) {
-                slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
+                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
                 cur_rec = slot;  // read again only while internal
                 descending = slot < kSlotBadChild;
             }
         } else {
             while (descending) {
-                slot = P.records[descend_index(px, py, pz, cur, min(cur_rec, P.n_records - 1u))];
+                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
                 depth += 1;
                 cur_rec = slot;
                 descending = slot < kSlotBadChild && depth < kMaxDepth;
@@ -789,7 +795,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     if (table_depth < 4 || table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
     // 32-bit slot addressing: record * 8 + octant must fit in uint32
-    if (n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
+    if (n_records > (1ull << 27)) return set_error(NAVI_E_ARG, "record pool exceeds 2^27 records (4 GiB)");
     const int64_t n_rays = n_envs * rays_per_env;
     // 32-bit work indexing: every ray index times 3 must fit in uint32
     if (n_rays > 0x3fffffffLL || rays_per_env > 0x3fffffffLL)

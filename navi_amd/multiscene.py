@@ -110,7 +110,7 @@ class ResidentScenes:
             recs.append(rec)
             roff += rec.shape[0]
         if self.relaid_ok:
-            if roff > (1 << 29):  # navi_trace_relaid addresses slots with 32-bit record * 8 + octant
+            if roff > (1 << 27):  # navi_trace_relaid reads the pool through a 4 GiB buffer resource
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
@@ -210,7 +210,7 @@ class ResidentScenes:
     def _require_relaid(self) -> None:
         if not self.relaid_ok:
             raise RuntimeError("these scenes do not fit the device record layout "
-                               "(leaf semantic above 0x7fff or more than 2^29 records)")
+                               "(leaf semantic above 0x7fff or more than 2^27 records)")
 
     def _check(self, name: str, t: Any, dtype: Any, shape: tuple[int, ...], optional: bool = False) -> int | None:
         if t is None:
