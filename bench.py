@@ -326,9 +326,23 @@ def main() -> int:
     mean_steps = float(out_n.float().mean().item())
     hit_rate = float((out_s != 0).float().mean().item())
 
+    def per_launch(steps):
+        """Each launch between its own events (after the bracketed run): the spread."""
+        stream = torch.cuda.current_stream(dev)
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        evs[0].record(stream)
+        for k in range(steps):
+            step("relaid")
+            evs[k + 1].record(stream)
+        torch.cuda.synchronize()
+        return np.array([evs[k].elapsed_time(evs[k + 1]) for k in range(steps)])
+
     ms_raw = timed("raw", max(1, args.steps // 4), 1) if not args.no_raw else None
     ms = timed("relaid", args.steps, args.warmup)
     rays_per_s = n_rays / (ms / 1e3)
+    launches = per_launch(args.steps)
+    launch_ms = {"median": round(float(np.median(launches)), 4), "p10": round(float(np.percentile(launches, 10)), 4),
+                 "p90": round(float(np.percentile(launches, 90)), 4), "launches": int(launches.size)}
 
     alg_bytes = n_rays * (24 + 8) + 8 * total_words
     achieved_gbs = alg_bytes / (ms / 1e3) / 1e9
@@ -404,6 +418,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "launch_ms": launch_ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
