@@ -64,11 +64,15 @@ def _rotate(local, rot):
     return np.ascontiguousarray(d, np.float32)
 
 
-@pytest.mark.parametrize("az,el", [(32, 16), (24, 5)])
-def test_pose_rays_equal_explicit_rays(gpu, corpus, az, el):
+@pytest.mark.parametrize("az,el,depth", [(32, 16, None), (24, 5, None), (16, 8, 4), (16, 8, 5), (16, 8, 6)])
+def test_pose_rays_equal_explicit_rays(gpu, corpus, az, el, depth):
+    """Rays generated in the tracer from poses against the oracle and against the same
+    rays passed explicitly; at the default cell-table depth and at depths 4 to 6."""
     import torch
 
-    res = _resident(corpus)
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus], table_depth=depth)
     env_scene, pos, rot = _poses(corpus, 20, seed=az)
     local = oracle.ray_directions(az, el)
     dirs = _rotate(local, rot)
