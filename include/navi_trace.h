@@ -146,7 +146,7 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
  * traces scenes[env_scene ? env_scene[e] : 0] (at most 1024 scenes; `records`
  * holds n_records records with absolute child slots, see navi_relaid_scene;
- * root_tables holds n_scenes cell tables of depth table_depth, 8^table_depth
+ * cell_tables holds n_scenes cell tables of depth table_depth, 8^table_depth
  * entries each, scene s at s * 8^table_depth, from navi_build_cell_table).
  * Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
@@ -159,7 +159,7 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
  */
 int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                      int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
+                      int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth,
                       const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                       int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                       const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -179,7 +179,7 @@ int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_re
  * cos / sin values. Everything else as navi_trace_relaid.
  */
 int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                            int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
+                            int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth,
                             const int32_t* env_scene,
                             const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
                             int32_t elevation_bins, const float* local_dirs, const float* env_pos,
@@ -193,7 +193,7 @@ typedef struct navi_point_queries {
     uint64_t n_records;
     const navi_relaid_scene* scenes;
     int32_t n_scenes;
-    const uint64_t* root_tables;       /* cell tables as in navi_trace_relaid */
+    const uint64_t* cell_tables;       /* cell tables as in navi_trace_relaid */
     int32_t table_depth;
     const int32_t* point_scene;        /* [n_points] scene ids, or NULL: scene 0 */
     const float* points;               /* [n_points][3] */

@@ -74,7 +74,7 @@ class PointQueries(ctypes.Structure):
     """navi_point_queries (include/navi_trace.h)."""
 
     _fields_ = [("records", _vp), ("n_records", ctypes.c_uint64), ("scenes", _vp), ("n_scenes", ctypes.c_int32),
-                ("root_tables", _vp), ("table_depth", ctypes.c_int32), ("point_scene", _vp), ("points", _vp),
+                ("cell_tables", _vp), ("table_depth", ctypes.c_int32), ("point_scene", _vp), ("points", _vp),
                 ("n_points", ctypes.c_int64),
                 ("out_distances", _vp), ("out_semantics", _vp), ("out_kind", _vp)]
 

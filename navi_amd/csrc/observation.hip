@@ -54,7 +54,7 @@ struct PostParams {
     uint32_t n_records;
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
-    const uint64_t* __restrict__ root_table;  // cell tables, 8^table_depth entries per scene
+    const uint64_t* __restrict__ cell_table;  // cell tables, 8^table_depth entries per scene
     uint32_t table_depth;
     const int32_t* __restrict__ point_scene;  // [n_points] or null (scene 0)
     const float* __restrict__ points;         // [n_points][3]
@@ -92,7 +92,7 @@ __device__ void point_query(const PostParams& P, int32_t i) {
                     jy = 2u * jy + ((oct >> 1) & 1u);
                     jz = 2u * jz + (oct >> 2);
                 }
-                const uint64_t e = P.root_table[((((uint32_t)sc << D | jz) << D | jy) << D) | jx];
+                const uint64_t e = P.cell_table[((((uint32_t)sc << D | jz) << D | jy) << D) | jx];
                 slot = static_cast<uint32_t>(e);
                 depth = static_cast<int32_t>(e >> 32);
                 if (depth < static_cast<int32_t>(D)) {
@@ -296,15 +296,15 @@ int points_setup(PostParams& P, const navi_point_queries* Q) {
     if (Q->n_points < 0 || Q->n_points > (1LL << 30)) return set_error(NAVI_E_ARG, "n_points must be in [0, 2^30]");
     if (!Q->points || !Q->out_distances || !Q->out_semantics)
         return set_error(NAVI_E_ARG, "points and point outputs must be non-null");
-    if (Q->n_scenes <= 0 || !Q->scenes || !Q->records || !Q->root_tables)
-        return set_error(NAVI_E_ARG, "scene table, records and root_tables must be non-empty");
+    if (Q->n_scenes <= 0 || !Q->scenes || !Q->records || !Q->cell_tables)
+        return set_error(NAVI_E_ARG, "scene table, records and cell_tables must be non-empty");
     if (Q->table_depth < 4 || Q->table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (Q->n_records > (1ull << 29)) return set_error(NAVI_E_ARG, "record pool exceeds 2^29 records");
     P.records = Q->records;
     P.n_records = static_cast<uint32_t>(Q->n_records);
     P.scenes = Q->scenes;
     P.n_scenes = Q->n_scenes;
-    P.root_table = Q->root_tables;
+    P.cell_table = Q->cell_tables;
     P.table_depth = static_cast<uint32_t>(Q->table_depth);
     P.point_scene = Q->point_scene;
     P.points = Q->points;

@@ -83,7 +83,7 @@ struct RelaidParams {
     uint32_t n_records;  // records in the pool (child slots are absolute indices)
     const navi_relaid_scene* __restrict__ scenes;
     int32_t n_scenes;
-    const uint64_t* __restrict__ root_table;  // cell tables, 8^cell_depth entries per scene
+    const uint64_t* __restrict__ cell_table;  // cell tables, 8^cell_depth entries per scene
     uint32_t cell_depth;                      // D in [4, 7]: descents start at depth D
     const int32_t* __restrict__ env_scene;  // null: every env uses scene 0
     const int32_t* __restrict__ env_order;  // null: identity
@@ -502,7 +502,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     jz = append_bit(jz, gz);
                 }
             }
-            const uint64_t e = P.root_table[(((scene << D | jz) << D | jy) << D) | jx];
+            const uint64_t e = P.cell_table[(((scene << D | jz) << D | jy) << D) | jx];
             slot = static_cast<uint32_t>(e);
             depth = static_cast<int32_t>(e >> 32);
             if (depth < static_cast<int32_t>(D)) {
@@ -781,7 +781,7 @@ namespace navi {
 
 // Arguments shared by the two relaid entry points.
 int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                 int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth, const int32_t* env_scene,
+                 int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth, const int32_t* env_scene,
                  const int32_t* env_order, int64_t n_envs, int64_t rays_per_env, int32_t elevation_bins,
                  float* out_distances, int32_t* out_semantics, int32_t max_steps, float max_distance,
                  float hit_epsilon, int32_t* out_steps) {
@@ -791,7 +791,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     if (!(hit_epsilon == hit_epsilon)) return set_error(NAVI_E_ARG, "hit_epsilon must not be NaN");
     if (n_envs < 0 || rays_per_env < 0) return set_error(NAVI_E_ARG, "n_envs and rays_per_env must be non-negative");
     if (n_scenes <= 0 || !scenes || !records) return set_error(NAVI_E_ARG, "scene table must be non-empty");
-    if (!root_tables) return set_error(NAVI_E_ARG, "root_tables is required (navi_build_cell_table)");
+    if (!cell_tables) return set_error(NAVI_E_ARG, "cell_tables is required (navi_build_cell_table)");
     if (table_depth < 4 || table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
     // 32-bit slot addressing: record * 8 + octant must fit in uint32
@@ -807,7 +807,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     P.n_records = static_cast<uint32_t>(n_records);
     P.scenes = scenes;
     P.n_scenes = n_scenes;
-    P.root_table = root_tables;
+    P.cell_table = cell_tables;
     P.cell_depth = static_cast<uint32_t>(table_depth);
     P.env_scene = env_scene;
     P.env_order = env_order;
@@ -831,7 +831,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
 }  // namespace navi
 
 extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
-                                 int32_t n_scenes, const uint64_t* root_tables, int32_t table_depth,
+                                 int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth,
                                  const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
                                  int64_t rays_per_env, int32_t elevation_bins, const float* origins,
                                  const float* dirs, float* out_distances, int32_t* out_semantics,
@@ -839,7 +839,7 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
                                  int32_t* out_steps, void* stream) {
     using namespace navi;
     RelaidParams P;
-    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, table_depth, env_scene,
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, cell_tables, table_depth, env_scene,
                                   env_order, n_envs, rays_per_env, elevation_bins, out_distances, out_semantics,
                                   max_steps, max_distance, hit_epsilon, out_steps);
     if (code != NAVI_OK || P.n_rays == 0) return code;
@@ -851,7 +851,7 @@ extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, co
 
 extern "C" int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records,
                                        const navi_relaid_scene* scenes, int32_t n_scenes,
-                                       const uint64_t* root_tables, int32_t table_depth,
+                                       const uint64_t* cell_tables, int32_t table_depth,
                                        const int32_t* env_scene,
                                        const int32_t* env_order, int64_t n_envs, int64_t rays_per_env,
                                        int32_t elevation_bins, const float* local_dirs, const float* env_pos,
@@ -860,7 +860,7 @@ extern "C" int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_recor
                                        int32_t* out_steps, void* stream) {
     using namespace navi;
     RelaidParams P;
-    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, root_tables, table_depth, env_scene,
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, cell_tables, table_depth, env_scene,
                                   env_order, n_envs, rays_per_env, elevation_bins, out_distances, out_semantics,
                                   max_steps, max_distance, hit_epsilon, out_steps);
     if (code != NAVI_OK || P.n_rays == 0) return code;

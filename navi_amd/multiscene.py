@@ -125,7 +125,7 @@ class ResidentScenes:
                 self.table_depth = max(4, min(default_table_depth(len(scenes)), deepest + 1))
             tables = np.concatenate([_native.cell_table(allrec[:roff], int(rtable[i]["root_slot"]), self.table_depth)
                                      for i in range(len(scenes))])
-            self.root_tables = torch.from_numpy(tables.view(np.int64)).to(self.device)
+            self.cell_tables = torch.from_numpy(tables.view(np.int64)).to(self.device)
             self.n_records = int(roff)
             self.records = torch.from_numpy(allrec.view(np.int32).reshape(-1).copy()).to(self.device)
             self.relaid_table = torch.from_numpy(rtable.view(np.uint8).copy()).to(self.device)
@@ -183,7 +183,7 @@ class ResidentScenes:
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 code = _native.lib().navi_trace_relaid(
                     self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                    self.root_tables.data_ptr(), self.table_depth,
+                    self.cell_tables.data_ptr(), self.table_depth,
                     env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
                     int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
                     out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),
@@ -243,7 +243,7 @@ class ResidentScenes:
             stream = torch.cuda.current_stream(self.device).cuda_stream
             code = _native.lib().navi_trace_relaid_poses(
                 self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                self.root_tables.data_ptr(), self.table_depth, ptrs[0],
+                self.cell_tables.data_ptr(), self.table_depth, ptrs[0],
                 order.data_ptr() if order is not None else None, e, r,
                 int(elevation_bins or 0), ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], int(max_steps),
                 float(max_distance), float(hit_epsilon), ptrs[6], stream)
@@ -254,7 +254,7 @@ class ResidentScenes:
         p = int(points.shape[0])
         q = _native.PointQueries()
         q.records, q.n_records = self.records.data_ptr(), self.n_records
-        q.scenes, q.n_scenes, q.root_tables = self.relaid_table.data_ptr(), self.n_scenes, self.root_tables.data_ptr()
+        q.scenes, q.n_scenes, q.cell_tables = self.relaid_table.data_ptr(), self.n_scenes, self.cell_tables.data_ptr()
         q.table_depth = self.table_depth
         q.points = self._check("points", points, torch.float32, (p, 3))
         q.n_points = p

@@ -200,7 +200,7 @@ def cast_rays(
             stream = torch.cuda.current_stream(dev).cuda_stream
             code = _native.lib().navi_trace_relaid(
                 scenes.records.data_ptr(), scenes.n_records, scenes.relaid_table.data_ptr(), 1,
-                scenes.root_tables.data_ptr(), scenes.table_depth, None, None, n_envs, rays, int(elevation_bins),
+                scenes.cell_tables.data_ptr(), scenes.table_depth, None, None, n_envs, rays, int(elevation_bins),
                 origins.data_ptr(), dirs.data_ptr(), out_distances.data_ptr(), out_semantics.data_ptr(),
                 int(max_steps), float(max_distance), float(hit_epsilon),
                 out_steps.data_ptr() if out_steps is not None else None, stream,

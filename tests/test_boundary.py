@@ -156,12 +156,12 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
                                   None, None)
     assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
     code = lib.navi_trace_relaid(1, 1, 1, 1, None, 6, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
-    assert code == _native.NAVI_E_ARG and "root_tables" in _native.last_error()
+    assert code == _native.NAVI_E_ARG and "cell_tables" in _native.last_error()
     for depth in (3, 8):
         code = lib.navi_trace_relaid(1, 1, 1, 1, 1, depth, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None,
                                       None)
         assert code == _native.NAVI_E_ARG and "table_depth" in _native.last_error()
-    q = _native.PointQueries(records=1, n_records=1, scenes=1, n_scenes=1, root_tables=1, table_depth=3,
+    q = _native.PointQueries(records=1, n_records=1, scenes=1, n_scenes=1, cell_tables=1, table_depth=3,
                              points=1, n_points=1, out_distances=1, out_semantics=1)
     assert lib.navi_point_query(ctypes.byref(q), None) == _native.NAVI_E_ARG
     assert "table_depth" in _native.last_error()

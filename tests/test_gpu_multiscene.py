@@ -402,7 +402,7 @@ def test_relaid_env_order_entries_out_of_range_are_skipped(gpu, corpus):
     out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
     code = _native.lib().navi_trace_relaid(
         res.records.data_ptr(), res.n_records, res.relaid_table.data_ptr(), res.n_scenes,
-        res.root_tables.data_ptr(), res.table_depth, t_es.data_ptr(), order.data_ptr(), 6, 16 * 8, 8, t_o.data_ptr(),
+        res.cell_tables.data_ptr(), res.table_depth, t_es.data_ptr(), order.data_ptr(), 6, 16 * 8, 8, t_o.data_ptr(),
         t_d.data_ptr(), out_d.data_ptr(), out_s.data_ptr(), 64, 30.0, 0.01, None,
         torch.cuda.current_stream().cuda_stream)
     _native.check(code)
