@@ -237,8 +237,8 @@ def small_configs(dev):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--envs", type=int, default=1024)
     ap.add_argument("--resolution", type=int, default=1024)
     ap.add_argument("--scenes", type=int, default=16)
