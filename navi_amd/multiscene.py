@@ -6,6 +6,16 @@ The reference keeps one DAG tensor per backend and swaps it on scene rotation
 scene. Here all scenes live in one device word pool with a 40-byte descriptor
 each (``navi_scene_desc`` in ``include/navi_trace.h``) and an int32 scene id
 per env selects the DAG inside the kernel.
+
+Work order. The record-layout tracer hands out rays in env order, and a launch
+lasts until its slowest wave ends: a scene whose rays run long (rooms with flat
+floors give grazing rays of hundreds of steps) should start first, not last.
+``ResidentScenes`` therefore sorts envs by scene, with the scenes in descending
+order of their measured cost (mean steps per ray) once it knows them: the first
+multi-scene launch also counts steps per ray, reduces them per scene on the
+device and copies the sums back asynchronously; a later launch that finds the
+copy complete adopts the order (longest-processing-time-first scheduling).
+Results do not depend on the order.
 """
 
 from __future__ import annotations
@@ -56,7 +66,7 @@ class ResidentScenes:
 
     def __init__(self, scenes: Sequence[tuple[np.ndarray, Sequence[float], Sequence[float]]],
                  device: str | torch.device = "cuda", *, keep_words: bool = True,
-                 table_depth: int | None = None) -> None:
+                 table_depth: int | None = None, order_by_cost: bool = True) -> None:
         if not scenes:
             raise ValueError("at least one scene is required")
         if table_depth is not None and not 4 <= int(table_depth) <= 7:
@@ -132,6 +142,12 @@ class ResidentScenes:
             self.record_counts = [int(r.shape[0]) for r in recs]
         self._order_key = None
         self._order = None
+        # scene order by measured cost (module docstring)
+        self.order_by_cost = bool(order_by_cost) and self.n_scenes > 1
+        self.scene_cost: np.ndarray | None = None  # mean steps per ray, once measured
+        self._scene_rank: torch.Tensor | None = None  # [n_scenes + 1] position of each scene; unknown ids last
+        self._cost_pending: tuple[Any, torch.Tensor] | None = None  # (event, pinned [2, n_scenes + 1])
+        self._cost_version = 0
 
     @property
     def pool_bytes(self) -> int:
@@ -142,12 +158,61 @@ class ResidentScenes:
         return int(self.records.numel()) * 4 if self.relaid_ok else 0
 
     def env_order(self, env_scene: torch.Tensor) -> torch.Tensor:
-        """Envs sorted (stably) by scene id, cached per env_scene contents/version."""
-        key = (env_scene.data_ptr(), env_scene._version, tuple(env_scene.shape))
+        """Envs sorted (stably) by scene: by scene id, or, once the scenes' costs are
+        measured, by descending cost. Cached per env_scene contents/version."""
+        key = (env_scene.data_ptr(), env_scene._version, tuple(env_scene.shape), self._cost_version)
         if self._order_key != key:
-            self._order = torch.sort(env_scene.to(torch.int64), stable=True).indices.to(torch.int32)
+            if self._scene_rank is None:
+                sort_key = env_scene.to(torch.int64)
+            else:
+                n = self.n_scenes
+                known = (env_scene >= 0) & (env_scene < n)
+                sort_key = self._scene_rank[torch.where(known, env_scene, n).to(torch.int64)]
+            self._order = torch.sort(sort_key, stable=True).indices.to(torch.int32)
             self._order_key = key
         return self._order
+
+    def _cost_steps(self, out_steps: Any, e: int, r: int, sort_by_scene: bool) -> tuple[Any, bool]:
+        """The steps tensor for a launch and whether the launch measures the scenes' costs."""
+        if not (self.order_by_cost and sort_by_scene) or self.scene_cost is not None or self._cost_pending is not None:
+            return out_steps, False
+        if out_steps is None:
+            out_steps = torch.empty((e, r), dtype=torch.int32, device=self.device)
+        return out_steps, True
+
+    def _start_cost_readback(self, steps: torch.Tensor, env_scene: torch.Tensor) -> None:
+        """Per-scene step sums and ray counts of the launch just queued, copied to pinned
+        host memory behind an event on the current stream (no wait here)."""
+        n = self.n_scenes
+        with torch.cuda.device(self.device):
+            idx = torch.where((env_scene >= 0) & (env_scene < n), env_scene, n).to(torch.int64)
+            sums = torch.zeros(n + 1, dtype=torch.int64, device=self.device)
+            sums.index_add_(0, idx, steps.sum(dim=1, dtype=torch.int64))
+            rays = torch.bincount(idx, minlength=n + 1) * int(steps.shape[1])
+            host = torch.empty((2, n + 1), dtype=torch.int64, pin_memory=True)
+            host[0].copy_(sums, non_blocking=True)
+            host[1].copy_(rays, non_blocking=True)
+            event = torch.cuda.Event()
+            event.record()
+        self._cost_pending = (event, host)
+
+    def _poll_cost(self) -> None:
+        """Adopt the measured scene costs if their copy has completed (never waits)."""
+        if self._cost_pending is None or not self._cost_pending[0].query():
+            return
+        host = self._cost_pending[1].numpy()
+        self._cost_pending = None
+        n = self.n_scenes
+        sums, rays = host[0, :n].astype(np.float64), host[1, :n]
+        cost = np.full(n, np.nan)
+        np.divide(sums, rays, out=cost, where=rays > 0)
+        cost[np.isnan(cost)] = np.nanmean(cost) if np.any(rays > 0) else 0.0  # unmeasured scenes
+        rank = np.empty(n + 1, np.int64)
+        rank[np.argsort(-cost, kind="stable")] = np.arange(n)
+        rank[n] = n
+        self.scene_cost = cost
+        self._scene_rank = torch.from_numpy(rank).to(self.device)
+        self._cost_version += 1
 
     def cast_rays(self, env_scene: torch.Tensor, origins: torch.Tensor, dirs: torch.Tensor,
                   out_distances: torch.Tensor, out_semantics: torch.Tensor, max_steps: int,
@@ -160,7 +225,9 @@ class ResidentScenes:
         ``kernel="relaid"`` (default) runs the device-layout tracer; ``"raw"`` walks the
         reference word layout (and is the one that can fill ``out_words``). Both give
         identical per-ray results. ``elevation_bins`` declares the canonical
-        ``az * El + el`` ray layout for angular tiling."""
+        ``az * El + el`` ray layout for angular tiling. ``sort_by_scene`` hands the
+        envs to the kernel grouped by scene, costliest scenes first once their costs
+        are measured (the first such launch counts steps per ray for that)."""
         e, r = int(origins.shape[0]), int(origins.shape[1])
         for name, t, dt, shape in (("origins", origins, torch.float32, (e, r, 3)),
                                    ("dirs", dirs, torch.float32, (e, r, 3)),
@@ -178,7 +245,9 @@ class ResidentScenes:
         if not (math.isfinite(float(max_distance)) and float(max_distance) > 0.0):
             raise RuntimeError("max_distance must be a finite positive float")
         if kernel == "relaid" and out_words is None and self.relaid_ok:
+            self._poll_cost()
             order = self.env_order(env_scene) if sort_by_scene else None
+            out_steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
             with torch.cuda.device(self.device):
                 stream = torch.cuda.current_stream(self.device).cuda_stream
                 code = _native.lib().navi_trace_relaid(
@@ -190,6 +259,8 @@ class ResidentScenes:
                     float(max_distance), float(hit_epsilon),
                     out_steps.data_ptr() if out_steps is not None else None, stream)
             _native.check(code)
+            if measure:
+                self._start_cost_readback(out_steps, env_scene)
             return
         if kernel not in ("relaid", "raw"):
             raise ValueError(f"unknown kernel {kernel!r}")
@@ -238,7 +309,10 @@ class ResidentScenes:
                 self._check("out_distances", out_distances, torch.float32, (e, r)),
                 self._check("out_semantics", out_semantics, torch.int32, (e, r)),
                 self._check("out_steps", out_steps, torch.int32, (e, r), optional=True)]
+        self._poll_cost()
         order = self.env_order(env_scene) if sort_by_scene else None
+        steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
+        ptrs[6] = steps.data_ptr() if steps is not None else None
         with torch.cuda.device(self.device):
             stream = torch.cuda.current_stream(self.device).cuda_stream
             code = _native.lib().navi_trace_relaid_poses(
@@ -248,6 +322,8 @@ class ResidentScenes:
                 int(elevation_bins or 0), ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], int(max_steps),
                 float(max_distance), float(hit_epsilon), ptrs[6], stream)
         _native.check(code)
+        if measure:
+            self._start_cost_readback(steps, env_scene)
 
     def _point_queries(self, points, out_distances, out_semantics, point_scene, out_kind, prefix=""):
         self._require_relaid()

@@ -458,3 +458,48 @@ def test_relaid_randomized_sweep(gpu, seed):
                         max_distance, hit_epsilon=eps)
     _compare(_run(res, env_scene, o, d, max_steps, max_distance, hit_epsilon=eps), ref, max_distance,
              f"sweep{seed}")
+
+
+def test_scene_order_follows_measured_cost(gpu, corpus):
+    """The first sorted launch counts steps per ray (also when the caller asks for
+    none) and reduces them per scene on the device; a later launch adopts the
+    costs and hands out the costliest scenes' envs first, unknown scene ids last.
+    Results are the oracle's in either order."""
+    import torch
+
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    env_scene, o, d = _rays(corpus, 24, 16, 8, seed=17)
+    env_scene[[3, 11]] = [-1, len(corpus)]
+    n = len(corpus)
+    known = (env_scene >= 0) & (env_scene < n)
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene[known], o[known], d[known], 160, 30.0)
+    dev = res.device
+    t_es = torch.from_numpy(env_scene).to(dev)
+    t_o = torch.from_numpy(np.ascontiguousarray(o)).to(dev)
+    t_d = torch.from_numpy(np.ascontiguousarray(d)).to(dev)
+    out_d = torch.full(o.shape[:2], -7.0, device=dev)
+    out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+    out_n = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, 160, 30.0, elevation_bins=8)  # measures
+    torch.cuda.synchronize()
+    assert res.scene_cost is None  # adopted by the next launch
+    first = (out_d.cpu().numpy(), out_s.cpu().numpy())
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, 160, 30.0, out_steps=out_n, elevation_bins=8)
+    torch.cuda.synchronize()
+    assert res.scene_cost is not None
+    got = (out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), None)
+    _compare(tuple(g[known] for g in got[:3]) + (None,), ref, 30.0, "cost-ordered")
+    assert np.isnan(got[0][~known]).all() and (got[1][~known] == 0).all() and (got[2][~known] == 0).all()
+    assert np.array_equal(first[0].view(np.uint32), got[0].view(np.uint32))
+    assert np.array_equal(first[1], got[1])
+    for s in range(n):
+        m = env_scene[known] == s
+        if m.any():
+            assert res.scene_cost[s] == pytest.approx(float(ref["steps"][m].mean()), rel=1e-12, abs=0)
+    pos = np.empty(n, np.int64)
+    pos[np.argsort(-res.scene_cost, kind="stable")] = np.arange(n)
+    key = np.where(known, pos[np.clip(env_scene, 0, n - 1)], n)
+    assert np.array_equal(res.env_order(t_es).cpu().numpy(), np.argsort(key, kind="stable"))
