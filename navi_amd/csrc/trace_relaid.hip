@@ -5,7 +5,7 @@
 //
 // Execution model (CDNA4, wave64):
 //   * persistent waves: the grid holds as many workgroups as the chip keeps
-//     resident; waves claim work units (256 rays = four 8 x 8 tiles, or one
+//     resident; waves claim work units (128 rays = two 8 x 8 tiles, or one
 //     tile for batches too small to fill the chip) from a per-stream counter
 //     pair, the last wave rearming it; without a counter (more than 256
 //     streams) wave w takes 64-ray chunks w, w + W, ...;
@@ -109,7 +109,7 @@ struct RelaidParams {
     uint32_t n_chunks;
     uint32_t* __restrict__ queue;  // [next unit, finished waves], or null: static schedule
     uint32_t n_units;              // work units of unit_rays rays
-    uint32_t unit_rays;            // 256 (4 tiles), or 64 for batches too small to fill the chip
+    uint32_t unit_rays;            // 128 (2 tiles), or 64 for batches too small to fill the chip
 };
 
 // Work index q -> ray id (env * R + r).
@@ -139,7 +139,9 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
 
 constexpr uint32_t kRefillMin = 8;
 constexpr uint32_t kLeafRun = 1;  // leaf-cache steps taken after a leaf step
-constexpr uint32_t kUnitRays = 256;  // rays per dynamically claimed work unit (4 tiles)
+// rays per dynamically claimed work unit (2 tiles): larger units leave more rays
+// held by one wave when the queue runs dry, smaller ones cost more claims
+constexpr uint32_t kUnitRays = 128;
 constexpr uint32_t kSmallUnitRays = 64;  // one tile, for small batches
 
 // A scene as the kernel reads it, staged in LDS once per workgroup so a lane
