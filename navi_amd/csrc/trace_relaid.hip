@@ -274,9 +274,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     float t = 0.f, dist = 0.f;
     int32_t sem = 0, step = 0;
     uint32_t scene = 0;  // this ray's scene (an index into lds_scenes)
-    Box lf{}, vd{}, pre{};
+    Box lf{}, vd{};
+    // The prefix cache (kernel.cu:120-132, 154-163) as the cell's depth-4
+    // indices x | y << 4 | z << 8. The plane kernels keep no box for it: the
+    // plane lookup of p decides containment in integers. Without planes the
+    // box is kept (kDepth = 0) or rebuilt by four splits (planes switched off
+    // for the launch).
+    Box pre{};
     uint32_t lf_slot = 0;
-    uint32_t pre_cell = 0;  // the prefix cell's depth-4 indices x | y << 4 | z << 8 (split path)
+    uint32_t pre_cell = 0;
     bool lf_ok = false, vd_ok = false, pre_ok = false;
 
     while (true) {
@@ -396,7 +402,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         const bool hit_vd = vd_ok && in_box_strict(px, py, pz, vd);
         const bool outside = !hit_vd && !in_box(px, py, pz, dom);
         const bool hit_lf = !hit_vd && !outside && lf_ok && in_box(px, py, pz, lf);
-        const bool use_pre = pre_ok && in_box(px, py, pz, pre);
         bool descending = has_ray && !(hit_vd || outside || hit_lf);
         Box cur = dom;
         uint32_t cur_rec = 0;
@@ -420,17 +425,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             const float* ply = plx + kAxis;
             const float* plz = ply + kAxis;
             uint32_t jx = 0, jy = 0, jz = 0;
+            bool use_pre;
             if (kPlanes && planes) {
                 const float4 scale = *reinterpret_cast<const float4*>(hdr);
                 jx = plane_cell(px, dom.x0, scale.x, plx, kCells, cur.x0, cur.x1);
                 jy = plane_cell(py, dom.y0, scale.y, ply, kCells, cur.y0, cur.y1);
                 jz = plane_cell(pz, dom.z0, scale.z, plz, kCells, cur.z0, cur.z1);
-                // p lies in the prefix cell, so only its upper faces can put the
-                // looked-up cell outside it
-                if (use_pre && !(px < pre.x1 && py < pre.y1 && pz < pre.z1)) {  // rare
-                    const bool fx = px == pre.x1 && cur.x0 == px;
-                    const bool fy = py == pre.y1 && cur.y0 == py;
-                    const bool fz = pz == pre.z1 && cur.z0 == pz;
+                // The prefix cell holds p, faces included (kernel.cu:120-132),
+                // when per axis p's cell lies in it or p is on its upper face,
+                // where p's cell starts (p == its lower plane). The domain's
+                // upper face is inside: there p's cell is the last one.
+                constexpr uint32_t sh = kPD - kPrefixDepth;
+                const uint32_t kx = pre_cell & 15u, ky = (pre_cell >> 4) & 15u, kz = pre_cell >> 8;
+                const bool fx = jx == ((kx + 1u) << sh) && px == cur.x0;
+                const bool fy = jy == ((ky + 1u) << sh) && py == cur.y0;
+                const bool fz = jz == ((kz + 1u) << sh) && pz == cur.z0;
+                use_pre = pre_ok && ((jx >> sh) == kx || fx) && ((jy >> sh) == ky || fy) && ((jz >> sh) == kz || fz);
+                // on an upper face the descent from the prefix cell stays in it
+                if (use_pre && (fx || fy || fz)) {  // rare
                     jx -= fx ? 1u : 0u;
                     jy -= fy ? 1u : 0u;
                     jz -= fz ? 1u : 0u;
@@ -459,6 +471,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     jz = append_bit(jz, gz);
                 }
             } else {
+                if (kPlanes && pre_ok) {  // planes off for this launch: rebuild the prefix box
+                    pre = dom;
+                    for (int l = 0; l < kPrefixDepth; ++l) {
+                        const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
+                        split_box(pre, ((pre_cell >> b) & 1u) | (((pre_cell >> (4u + b)) & 1u) << 1) |
+                                           (((pre_cell >> (8u + b)) & 1u) << 2));
+                    }
+                }
+                use_pre = pre_ok && in_box(px, py, pz, pre);
                 // a prefix descent starts from the cached cell, a fresh one
                 // from the domain, four levels up
                 cur.x0 = use_pre ? pre.x0 : dom.x0;
@@ -532,19 +553,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             if (save) {
                 const uint32_t sh = D - kPrefixDepth;
                 const uint32_t kx = jx >> sh, ky = jy >> sh, kz = jz >> sh;
-                if (kPlanes && planes) {
-                    const uint32_t up = kPD - kPrefixDepth;
-                    const uint32_t w = 1u << up;
-                    const uint32_t ax = kx << up, ay = ky << up, az = kz << up;
-                    pre = Box{plx[ax], ply[ay], plz[az], plx[ax + w], ply[ay + w], plz[az + w]};
-                } else {
+                if (!kPlanes) {
                     pre = dom;
                     for (int l = 0; l < kPrefixDepth; ++l) {
                         const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
                         split_box(pre, ((kx >> b) & 1u) | (((ky >> b) & 1u) << 1) | (((kz >> b) & 1u) << 2));
                     }
                 }
-                if (!(kPlanes && planes)) pre_cell = kx | (ky << 4) | (kz << 8);
+                pre_cell = kx | (ky << 4) | (kz << 8);
                 pre_ok = true;
             }
             cur_rec = slot;
