@@ -20,7 +20,8 @@
 //     then the step resolves with selects, and lanes whose step was a leaf
 //     take one more step if the leaf cache answers it alone;
 //   * work order: envs in the order given (callers sort them by scene so the
-//     resident scenes stream through L2 / MALL one or two at a time) and, when
+//     resident scenes stream through L2 / MALL one or two at a time, the
+//     costliest scenes first so the launch ends on short rays) and, when
 //     the elevation count is a multiple of 8, 8 x 8 (az x el) tiles of the
 //     canonical az*El + el ray layout, so a wave's rays are angular
 //     neighbours that share DAG nodes.
