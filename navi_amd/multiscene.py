@@ -174,7 +174,8 @@ class ResidentScenes:
 
     def _cost_steps(self, out_steps: Any, e: int, r: int, sort_by_scene: bool) -> tuple[Any, bool]:
         """The steps tensor for a launch and whether the launch measures the scenes' costs."""
-        if not (self.order_by_cost and sort_by_scene) or self.scene_cost is not None or self._cost_pending is not None:
+        if (not (self.order_by_cost and sort_by_scene) or self.scene_cost is not None
+                or self._cost_pending is not None or e * r == 0):
             return out_steps, False
         if out_steps is None:
             out_steps = torch.empty((e, r), dtype=torch.int32, device=self.device)
@@ -204,6 +205,8 @@ class ResidentScenes:
         self._cost_pending = None
         n = self.n_scenes
         sums, rays = host[0, :n].astype(np.float64), host[1, :n]
+        if not np.any(rays > 0):  # no ray of a known scene: measure on a later launch
+            return
         cost = np.full(n, np.nan)
         np.divide(sums, rays, out=cost, where=rays > 0)
         cost[np.isnan(cost)] = np.nanmean(cost) if np.any(rays > 0) else 0.0  # unmeasured scenes

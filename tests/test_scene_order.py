@@ -86,3 +86,16 @@ def test_measurement_uses_the_callers_steps_once():
     res._cost_pending = (_Pending(), torch.zeros((2, 3), dtype=torch.int64))
     steps, measure = res._cost_steps(None, 2, 8, True)  # one measurement at a time
     assert steps is None and not measure
+
+
+def test_empty_measurements_are_retried():
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes(_scenes(2), "cpu")
+    assert res._cost_steps(None, 0, 8, True) == (None, False)  # empty batches measure nothing
+    # only unknown scene ids (last column) were traced: nothing adopted, measured again later
+    res._cost_pending = (_Done(), torch.tensor([[0, 0, 50], [0, 0, 10]], dtype=torch.int64))
+    res._poll_cost()
+    assert res.scene_cost is None and res._cost_pending is None
+    steps, measure = res._cost_steps(None, 2, 8, True)
+    assert measure and tuple(steps.shape) == (2, 8)
