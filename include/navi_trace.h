@@ -124,7 +124,7 @@ int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root
 /*
  * Cell table of one scene (no reference counterpart; host memory in and out):
  * 8^depth u64 entries over the 2^depth x 2^depth x 2^depth grid of the cells
- * at that depth, depth in [4, 7]. Entry (iz << 2 depth) | (iy << depth) | ix
+ * at that depth, depth in [4, 7]. Entry (iz << (2 * depth)) | (iy << depth) | ix
  * (the cell whose octant at level l has x bit (ix >> (depth - 1 - l)) & 1, y
  * and z likewise) = the slot a descent from the root meets within `depth`
  * levels (bits 31..0: a leaf, void or out-of-range slot, or the record of the
@@ -133,7 +133,7 @@ int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root
  * (absolute record indices in a pool), so record slots in the table are
  * absolute too. The tracer's descents start at the table's depth: deeper
  * tables save record reads and cost 8x the memory per level (depth 6: 2 MiB
- * per scene).
+ * per scene, depth 7: 16 MiB).
  */
 int navi_build_cell_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot, int32_t depth,
                           uint64_t* out_table);
@@ -151,9 +151,10 @@ int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t 
  * Per-ray results are identical
  * to navi_cast_rays / navi_cast_rays_multi on the same DAG. env_order
  * (optional, a permutation of [0, n_envs); an entry outside that range is
- * skipped, its rays left unwritten) is the order envs are swept in —
- * pass envs sorted by scene id so resident scenes stream through the caches
- * one at a time. elevation_bins > 0 (a multiple of 8 dividing rays_per_env / 8)
+ * skipped, its rays left unwritten) is the order envs are swept in — pass
+ * envs grouped by scene, so resident scenes stream through the caches one at
+ * a time, with the scenes of most steps per ray first: a launch lasts until
+ * its slowest wave ends, so long rays should not start last. elevation_bins > 0 (a multiple of 8 dividing rays_per_env / 8)
  * declares the canonical az*El + el ray layout (projects/environment/src/
  * navi_environment/backends/sdfdag_backend.py:205-221) so rays are traced in
  * 8 x 8 angular tiles. Outputs as in navi_cast_rays.
