@@ -153,12 +153,14 @@ struct SceneLds {
     uint32_t pad;
 };
 constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
-// Split planes of the first D levels, per scene: the scales n / (hi - lo) of
+// Split planes of the first P levels, per scene: the scales n / (hi - lo) of
 // x, y and z and a pad float, then per axis the n + 1 planes P_0 = lo, ...,
-// P_n = hi of the n = 2^D depth-D cells and a pad float, the scene's block
-// rounded up to 16 bytes. Launches whose scene table and planes would exceed
-// kPlaneLds bytes skip the planes.
-constexpr size_t kPlaneLds = 26624;
+// P_n = hi of the n = 2^P depth-P cells and a pad float, the scene's block
+// rounded up to 16 bytes. A launch stages the deepest P (at most 6, at most
+// two levels above the cell table) whose scene table and planes fit kPlaneLds
+// bytes, else none: 22 KiB keeps seven 256-thread workgroups (7 waves per
+// SIMD) within a CU's 160 KiB of LDS.
+constexpr size_t kPlaneLds = 22528;
 __host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
 __host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) { return (4u + 3u * axis_stride(depth) + 3u) & ~3u; }
 
@@ -206,11 +208,15 @@ __device__ __forceinline__ uint32_t plane_cell(float p, float lo0, float scale, 
     return j0 + (up ? 1u : 0u);
 }
 
-// kDepth > 0: the cell-table depth, with the scenes' split planes staged in
-// LDS; kDepth = 0: the depth is P.cell_depth and cells come from splits.
-template <int kDepth, bool kPoses>
+// kPD > 0: the scenes' split planes of the first kPD levels staged in LDS and
+// kDepth the cell-table depth (kPD <= kDepth <= kPD + 2: a depth-kDepth cell is
+// kDepth - kPD splits below its depth-kPD cell); kPD = 0: no planes, the table
+// depth is P.cell_depth and cells come from splits.
+template <int kDepth, int kPD, bool kPoses>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
-    constexpr bool kPlanes = kDepth > 0;
+    constexpr bool kPlanes = kPD > 0;
+    static_assert(!kPlanes || (kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7),
+                  "planes of 4..6 levels, the table at most two levels below them");
     extern __shared__ SceneLds lds_scenes[];
     float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
     // `tame`: every scene box has coordinates below 2^100 in magnitude, so
@@ -234,9 +240,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     // `planes`: every scene's depth-D cells can be located from its planes
     int planes = kPlanes ? 1 : 0;
     const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
-    // The planes go down to depth kPD = min(D, 6) (deeper ones would crowd LDS);
-    // a depth-7 cell is one split below its depth-6 cell.
-    constexpr uint32_t kPD = kPlanes ? (kDepth < 6 ? kDepth : 6) : 0u;
     constexpr uint32_t kAxis = kPlanes ? axis_stride(kPD) : 0u;    // floats per axis
     constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
     constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
@@ -532,12 +535,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             if (depth < static_cast<int32_t>(D)) {
                 // leaf / void / fault above depth D: its box is the one after
                 // `depth` splits
-                if (kPlanes && planes) {  // depth < D <= 7, so depth <= kPD
-                    const uint32_t sh = D - static_cast<uint32_t>(depth);
-                    const uint32_t up = kPD - static_cast<uint32_t>(depth);
+                if (kPlanes && planes) {
+                    // the planes give the box down to depth kPD, splits the rest
+                    const uint32_t dp = min(static_cast<uint32_t>(depth), static_cast<uint32_t>(kPD));
+                    const uint32_t sh = D - dp;
+                    const uint32_t up = kPD - dp;
                     const uint32_t w = 1u << up;
                     const uint32_t kx = (jx >> sh) << up, ky = (jy >> sh) << up, kz = (jz >> sh) << up;
                     cur = Box{plx[kx], ply[ky], plz[kz], plx[kx + w], ply[ky + w], plz[kz + w]};
+                    if (kDepth > kPD + 1) {  // depth can lie between kPD and D
+#pragma unroll 1
+                        for (uint32_t l = static_cast<uint32_t>(kPD); l < static_cast<uint32_t>(depth); ++l) {
+                            const uint32_t b = D - 1u - l;
+                            split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
+                        }
+                    }
                 } else {
                     cur = dom;
 #pragma unroll 1
@@ -749,20 +761,33 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.unit_rays = kUnitRays;
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
-    const size_t plane_bytes = static_cast<size_t>(scene_stride(P.cell_depth < 6 ? P.cell_depth : 6)) * sizeof(float);
-    const bool use_planes = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + plane_bytes) <= kPlaneLds;
-    const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (use_planes ? plane_bytes : 0));
-    const bool poses = P.local_dirs != nullptr;
-    const int depth = use_planes ? static_cast<int>(P.cell_depth) : 0;
-    void (*kernel)(RelaidParams) = nullptr;
-    switch (depth) {
-        case 4: kernel = poses ? trace_relaid_kernel<4, true> : trace_relaid_kernel<4, false>; break;
-        case 5: kernel = poses ? trace_relaid_kernel<5, true> : trace_relaid_kernel<5, false>; break;
-        case 6: kernel = poses ? trace_relaid_kernel<6, true> : trace_relaid_kernel<6, false>; break;
-        case 7: kernel = poses ? trace_relaid_kernel<7, true> : trace_relaid_kernel<7, false>; break;
-        default: kernel = poses ? trace_relaid_kernel<0, true> : trace_relaid_kernel<0, false>; break;
+    // Split planes of the deepest P <= min(D, 6), at most two levels above the
+    // table, whose LDS (with the scene table) fits kPlaneLds; none if no P does.
+    const uint32_t D = P.cell_depth;
+    int pd = 0;
+    for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p) {
+        if (static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= kPlaneLds) {
+            pd = p;
+            break;
+        }
     }
-    const auto key = std::make_pair(2 * depth + static_cast<int>(poses), lds);
+    const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (pd ? scene_stride(pd) * sizeof(float) : 0));
+    const bool poses = P.local_dirs != nullptr;
+    void (*kernel)(RelaidParams) = nullptr;
+#define NAVI_RELAID(d, p) (poses ? trace_relaid_kernel<d, p, true> : trace_relaid_kernel<d, p, false>)
+    switch (pd * 8 + static_cast<int>(D)) {
+        case 4 * 8 + 4: kernel = NAVI_RELAID(4, 4); break;
+        case 4 * 8 + 5: kernel = NAVI_RELAID(5, 4); break;
+        case 4 * 8 + 6: kernel = NAVI_RELAID(6, 4); break;
+        case 5 * 8 + 5: kernel = NAVI_RELAID(5, 5); break;
+        case 5 * 8 + 6: kernel = NAVI_RELAID(6, 5); break;
+        case 5 * 8 + 7: kernel = NAVI_RELAID(7, 5); break;
+        case 6 * 8 + 6: kernel = NAVI_RELAID(6, 6); break;
+        case 6 * 8 + 7: kernel = NAVI_RELAID(7, 6); break;
+        default: kernel = NAVI_RELAID(0, 0); break;
+    }
+#undef NAVI_RELAID
+    const auto key = std::make_pair(2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses), lds);
     int grid_blocks = 0;
     {
         std::lock_guard<std::mutex> lock(g_queue_mu);

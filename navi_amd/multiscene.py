@@ -32,13 +32,22 @@ from . import _native
 
 # The tracer stages each scene's split planes in LDS when the scene table and
 # planes of a launch fit in this many bytes (kPlaneLds in trace_relaid.hip):
-# 32 bytes per scene plus scene_stride(D) floats.
-PLANE_LDS_BYTES = 26624
+# 32 bytes per scene plus scene_stride(P) floats, P the planes' depth.
+PLANE_LDS_BYTES = 22528
 
 
 def _plane_bytes(depth: int) -> int:
-    depth = min(depth, 6)  # deeper cells are one split below their depth-6 cell
     return 4 * ((4 + 3 * ((1 << depth) + 2) + 3) & ~3)
+
+
+def plane_depth(n_scenes: int, table_depth: int) -> int:
+    """The split-plane depth the tracer uses for ``n_scenes`` scenes and cell tables of
+    ``table_depth`` (launch_relaid in trace_relaid.hip): the deepest P <= min(D, 6), at
+    most two levels above the tables, whose planes fit ``PLANE_LDS_BYTES``; 0 for none."""
+    for p in range(min(table_depth, 6), max(4, table_depth - 2) - 1, -1):
+        if n_scenes * (32 + _plane_bytes(p)) <= PLANE_LDS_BYTES:
+            return p
+    return 0
 
 
 # Cell tables take 8 bytes per cell: 2 MiB per scene at depth 6, 16 MiB at 7.
@@ -46,12 +55,10 @@ TABLE_BYTES_BUDGET = 256 << 20
 
 
 def default_table_depth(n_scenes: int) -> int:
-    """The deepest cell table (at most 7) whose split planes fit the tracer's LDS budget
-    for ``n_scenes`` scenes and whose tables stay within ``TABLE_BYTES_BUDGET``; 4 when
-    none does (16 scenes: 7; up to 31: 6; up to 57: 5)."""
+    """The deepest cell table (at most 7) whose tables stay within
+    ``TABLE_BYTES_BUDGET``: 7 for up to 16 scenes, 6 up to 128, 5 up to 1024."""
     for depth in (7, 6, 5):
-        if (n_scenes * (32 + _plane_bytes(depth)) <= PLANE_LDS_BYTES
-                and n_scenes * 8 ** depth * 8 <= TABLE_BYTES_BUDGET):
+        if n_scenes * 8 ** depth * 8 <= TABLE_BYTES_BUDGET:
             return depth
     return 4
 

@@ -265,11 +265,11 @@ def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
     """100 resident scenes (more than the launch keeps split planes for in LDS),
     and domains too narrow for their magnitude (float split planes collapse),
     both located by in-register splits instead of the plane lookup."""
-    from navi_amd.multiscene import PLANE_LDS_BYTES, ResidentScenes, _plane_bytes
+    from navi_amd.multiscene import ResidentScenes, plane_depth
 
     many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(100)]
     res = ResidentScenes(many)
-    assert res.table_depth == 4 and 100 * (32 + _plane_bytes(4)) > PLANE_LDS_BYTES
+    assert res.table_depth == 6 and plane_depth(100, 6) == 0
     env_scene, o, d = _rays(corpus, 24, 16, 16, seed=31)
     env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 100
     ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 128, 30.0)
@@ -325,19 +325,20 @@ def test_relaid_every_table_depth(gpu, corpus, depth):
     _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, f"depth{depth}/narrow")
 
 
-@pytest.mark.parametrize("depth", [5, 6])
-def test_relaid_deep_tables_without_planes(gpu, corpus, depth):
-    """60 resident scenes with cell tables deeper than 4: more split planes than
-    the launch stages in LDS, so every cell comes from splits in registers."""
-    from navi_amd.multiscene import PLANE_LDS_BYTES, ResidentScenes, _plane_bytes
+@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (30, 6, 5), (60, 5, 4), (60, 6, 4), (100, 5, 0)])
+def test_relaid_tables_below_the_planes(gpu, corpus, n, depth, planes):
+    """Many resident scenes: the launch stages split planes of fewer levels than
+    the cell tables have (one or two levels below them come from splits in
+    registers), or none at all (every cell from splits)."""
+    from navi_amd.multiscene import ResidentScenes, plane_depth
 
-    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(60)]
-    assert 60 * (32 + _plane_bytes(depth)) > PLANE_LDS_BYTES
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(n)]
+    assert plane_depth(n, depth) == planes
     res = ResidentScenes(many, table_depth=depth)
     env_scene, o, d = _rays(corpus, 20, 16, 16, seed=50 + depth)
-    env_scene = (env_scene + 4 * np.arange(20, dtype=np.int32)) % 60
+    env_scene = (env_scene + 4 * np.arange(20, dtype=np.int32)) % n
     ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 200, 30.0)
-    _compare(_run(res, env_scene, o, d, 200, 30.0, elevation_bins=16), ref, 30.0, f"noplanes{depth}")
+    _compare(_run(res, env_scene, o, d, 200, 30.0, elevation_bins=16), ref, 30.0, f"planes{planes}/depth{depth}")
 
 
 @pytest.mark.parametrize("n", [31, 32])
