@@ -475,7 +475,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                     jz = append_bit(jz, gz);
                 }
             } else {
-                if (kPlanes && pre_ok) {  // planes off for this launch: rebuild the prefix box
+                if (kPlanes) {  // planes off for this launch: rebuild the prefix box
+                    // (also without a prefix, so that no box lives across steps)
                     pre = dom;
                     for (int l = 0; l < kPrefixDepth; ++l) {
                         const uint32_t b = static_cast<uint32_t>(kPrefixDepth - 1 - l);
