@@ -189,8 +189,14 @@ def dropin_timing(corpus, env_scene, t_o, t_d, args):
         ev1.record()
         torch.cuda.synchronize()
         ms = ev0.elapsed_time(ev1) / reps
+        # host wall time per call with a synchronize after each (Python checks included)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            call()
+            torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) / reps * 1e3
         result[kernel] = {"rays_per_s": round(result["rays"] / (ms / 1e3), 1), "ms": round(ms, 3),
-                          "first_call_s": round(first, 3)}
+                          "wall_ms": round(wall_ms, 3), "first_call_s": round(first, 3)}
     return result
 
 
