@@ -40,6 +40,17 @@ def _cache_dir() -> Path | None:
     return p
 
 
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def build_corpus(seeds, resolution, threads_total):
     from navi_amd import scenes as S
 
@@ -387,7 +398,7 @@ def main() -> int:
             times.append(time.perf_counter() - t)
         t_cpu = float(np.median(times))
         cpu = {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
-               "kind": "port",
+               "kind": "port", "cpu_model": _cpu_model(),
                "sample": f"{sample_text}, median of 2 timed runs after 1 warm-up"}
         gd = out_d.cpu().numpy()[sample]
         gs = out_s.cpu().numpy()[sample]
