@@ -94,6 +94,37 @@ def test_pose_rays_equal_explicit_rays(gpu, corpus, az, el, depth):
     assert np.array_equal(explicit[0].view(np.uint32), got[0].view(np.uint32))
 
 
+@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (60, 6, 4), (100, 5, 0)])
+def test_pose_rays_with_planes_above_the_tables(gpu, corpus, n, depth, planes):
+    """Rays from poses over many resident scenes, where the launch stages split planes
+    one or two levels above the cell tables, or none: against the oracle."""
+    import torch
+
+    from navi_amd.multiscene import ResidentScenes, plane_depth
+
+    many = [corpus[i % len(corpus)] for i in range(n)]
+    assert plane_depth(n, depth) == planes
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in many], table_depth=depth)
+    env_scene, pos, rot = _poses(corpus, 20, seed=n)
+    env_scene = ((env_scene + len(corpus) * np.arange(20)) % n).astype(np.int32)
+    local = oracle.ray_directions(16, 8)
+    dirs = _rotate(local, rot)
+    origins = np.ascontiguousarray(np.broadcast_to(pos[:, None, :], dirs.shape))
+    ref = _oracle_multi([c.words for c in many], [c.bbox_min_list + c.bbox_max for c in many],
+                        env_scene, origins, dirs, 160, 30.0)
+    dev = res.device
+    t = {k: torch.from_numpy(v).to(dev) for k, v in
+         (("es", env_scene), ("local", local), ("pos", pos), ("rot", rot))}
+    out_d = torch.full((20, 128), -7.0, device=dev)
+    out_s = torch.full((20, 128), -7, device=dev, dtype=torch.int32)
+    out_n = torch.full((20, 128), -7, device=dev, dtype=torch.int32)
+    res.cast_rays_poses(t["es"], t["local"], t["pos"], t["rot"], out_d, out_s, 160, 30.0, out_steps=out_n,
+                        elevation_bins=8)
+    torch.cuda.synchronize()
+    got = (out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), None)
+    _compare(got, ref, 30.0, f"poses/{n}/{depth}")
+
+
 def _point_cases(corpus, n, seed):
     rng = np.random.default_rng(seed)
     scene = rng.integers(0, len(corpus), n).astype(np.int32)
