@@ -250,7 +250,7 @@ class ResidentScenes:
             if t is not None and (t.device != self.device or t.dtype != dt or not t.is_contiguous()
                                   or tuple(t.shape) != (e, r)):
                 raise RuntimeError(f"{name} must be a contiguous {dt} tensor of shape {(e, r)}")
-        if int(max_steps) <= 0:
+        if not 0 < int(max_steps) <= 0x7FFFFFFF:  # an int32 in the C ABI
             raise RuntimeError("max_steps must be a positive integer")
         if not (math.isfinite(float(max_distance)) and float(max_distance) > 0.0):
             raise RuntimeError("max_distance must be a finite positive float")
@@ -311,6 +311,8 @@ class ResidentScenes:
         rotated by its yaw (``env_rot[e] = (cos, sin)``) from ``env_pos[e]``, the ray layout
         of ``sdfdag_backend.py:1300-1312``. Outputs ``[E, R]`` as ``cast_rays``."""
         self._require_relaid()
+        if not 0 < int(max_steps) <= 0x7FFFFFFF:  # an int32 in the C ABI
+            raise RuntimeError("max_steps must be a positive integer")
         e, r = int(env_pos.shape[0]), int(local_dirs.shape[0])
         ptrs = [self._check("env_scene", env_scene, torch.int32, (e,)),
                 self._check("local_dirs", local_dirs, torch.float32, (r, 3)),

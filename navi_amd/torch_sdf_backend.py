@@ -40,6 +40,7 @@ from . import _native
 
 _DIRECTION_NORM_EPS = 1e-4  # kernel.cuh:9
 HIT_EPSILON = 0.01  # kernel.cuh:7
+_INT32_MAX = 0x7FFFFFFF
 
 __all__ = ["cast_rays", "HIT_EPSILON"]
 
@@ -112,12 +113,13 @@ def validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics
         out_semantics.size(0) == origins.size(0) and out_semantics.size(1) == origins.size(1),
         "out_semantics must match the [Batch, Rays] shape of origins",
     )
-    _check(int(max_steps) > 0, "max_steps must be a positive integer")
+    # int32 in the native call (bindings.cpp:51): larger values do not convert
+    _check(0 < int(max_steps) <= _INT32_MAX, "max_steps must be a positive integer")
     _check(
         math.isfinite(_f32(max_distance)) and _f32(max_distance) > 0.0,
         "max_distance must be a finite positive float",
     )
-    _check(int(resolution) > 0, "resolution must be a positive integer")
+    _check(0 < int(resolution) <= _INT32_MAX, "resolution must be a positive integer")
     _validate_bounds(bbox_min, bbox_max)
     # One device for every operand: the kernel dereferences all of them.
     dev = dag_tensor.device
