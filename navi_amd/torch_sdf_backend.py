@@ -113,7 +113,7 @@ def validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics
         out_semantics.size(0) == origins.size(0) and out_semantics.size(1) == origins.size(1),
         "out_semantics must match the [Batch, Rays] shape of origins",
     )
-    # int32 in the native call (bindings.cpp:51): larger values do not convert
+    # int max_steps and int resolution in the native call (bindings.cpp:49,53)
     _check(0 < int(max_steps) <= _INT32_MAX, "max_steps must be a positive integer")
     _check(
         math.isfinite(_f32(max_distance)) and _f32(max_distance) > 0.0,

@@ -127,7 +127,7 @@ def test_native_layer_checks_cpu_tensors_before_launch():
     (64, 2 ** 31, "resolution must be a positive integer"),
 ])
 def test_native_layer_rejects_values_beyond_int32(max_steps, resolution, msg):
-    """The native call takes int32 step counts and resolutions (bindings.cpp:51-52):
+    """The native call takes int step counts and resolutions (bindings.cpp:49,53):
     larger values are rejected, not truncated."""
     with pytest.raises(RuntimeError, match=msg):
         torch_sdf_backend.validate_cast_inputs(*_inputs(), max_steps, 30.0, [0, 0, 0], [1, 1, 1], resolution)
