@@ -238,6 +238,7 @@ class ResidentScenes:
         ``az * El + el`` ray layout for angular tiling. ``sort_by_scene`` hands the
         envs to the kernel grouped by scene, costliest scenes first once their costs
         are measured (the first such launch counts steps per ray for that)."""
+        self._require_gpu()
         e, r = int(origins.shape[0]), int(origins.shape[1])
         for name, t, dt, shape in (("origins", origins, torch.float32, (e, r, 3)),
                                    ("dirs", dirs, torch.float32, (e, r, 3)),
@@ -288,7 +289,13 @@ class ResidentScenes:
 
     # ---- pose-driven tracing, point queries and the observation post-pass ----
 
+    def _require_gpu(self) -> None:
+        # the kernels dereference every pointer on the GPU: host tensors never reach them
+        if self.device.type != "cuda":
+            raise RuntimeError(f"tracing needs the scenes on a GPU device, not {self.device}")
+
     def _require_relaid(self) -> None:
+        self._require_gpu()
         if not self.relaid_ok:
             raise RuntimeError("these scenes do not fit the device record layout "
                                "(leaf semantic above 0x7fff or more than 2^27 records)")
@@ -379,6 +386,7 @@ class ResidentScenes:
         starvation, proximity, structure-band and forward-structure ratios) and
         ``out_collision [E]`` (int32). Defaults are the reference's
         (``sdfdag_backend.py:38,48-51``)."""
+        self._require_gpu()
         e = int(distances.shape[0])
         az, el = int(azimuth_bins), int(elevation_bins)
         o = _native.Observation()

@@ -99,3 +99,21 @@ def test_empty_measurements_are_retried():
     assert res.scene_cost is None and res._cost_pending is None
     steps, measure = res._cost_steps(None, 2, 8, True)
     assert measure and tuple(steps.shape) == (2, 8)
+
+
+def test_host_resident_scenes_refuse_to_trace():
+    """Scenes kept on the CPU (host logic only) never hand host pointers to the kernels."""
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes(_scenes(2), "cpu")
+    es = torch.zeros(1, dtype=torch.int32)
+    o = torch.zeros((1, 4, 3))
+    with pytest.raises(RuntimeError, match="GPU device"):
+        res.cast_rays(es, o, o, torch.zeros(1, 4), torch.zeros(1, 4, dtype=torch.int32), 8, 1.0)
+    with pytest.raises(RuntimeError, match="GPU device"):
+        res.cast_rays_poses(es, torch.zeros(4, 3), torch.zeros(1, 3), torch.zeros(1, 2), torch.zeros(1, 4),
+                            torch.zeros(1, 4, dtype=torch.int32), 8, 1.0)
+    with pytest.raises(RuntimeError, match="GPU device"):
+        res.point_query(torch.zeros(2, 3), torch.zeros(2), torch.zeros(2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="GPU device"):
+        res.observe(torch.zeros(1, 4), 2, 2, 1.0)
