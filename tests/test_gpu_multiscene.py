@@ -337,8 +337,21 @@ def test_relaid_tables_below_the_planes(gpu, corpus, n, depth, planes):
     res = ResidentScenes(many, table_depth=depth)
     env_scene, o, d = _rays(corpus, 20, 16, 16, seed=50 + depth)
     env_scene = (env_scene + 4 * np.arange(20, dtype=np.int32)) % n
-    ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 200, 30.0)
+    words = [s[0] for s in many]
+    bounds = [list(s[1]) + list(s[2]) for s in many]
+    ref = _oracle_multi(words, bounds, env_scene, o, d, 200, 30.0)
     _compare(_run(res, env_scene, o, d, 200, 30.0, elevation_bins=16), ref, 30.0, f"planes{planes}/depth{depth}")
+    # random rays from inside and around the domains, random directions (faces of
+    # void cells and of the cached prefix cell are crossed often)
+    rng = np.random.default_rng(n + depth)
+    lo = np.array([bounds[s][:3] for s in env_scene]) - 2.0
+    hi = np.array([bounds[s][3:] for s in env_scene]) + 2.0
+    o = rng.uniform(lo[:, None, :], hi[:, None, :], (20, 400, 3)).astype(np.float32)
+    d = rng.normal(size=(20, 400, 3))
+    d[:, :40, 0] = 0.0  # some rays parallel to the x planes
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    ref = _oracle_multi(words, bounds, env_scene, o, d, 300, 45.0)
+    _compare(_run(res, env_scene, o, d, 300, 45.0), ref, 45.0, f"planes{planes}/depth{depth}/random")
 
 
 @pytest.mark.parametrize("n", [31, 32])
