@@ -517,3 +517,70 @@ def test_scene_order_follows_measured_cost(gpu, corpus):
     pos[np.argsort(-res.scene_cost, kind="stable")] = np.arange(n)
     key = np.where(known, pos[np.clip(env_scene, 0, n - 1)], n)
     assert np.array_equal(res.env_order(t_es).cpu().numpy(), np.argsort(key, kind="stable"))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_relaid_random_scene_counts_and_depths(gpu, seed):
+    """Random scenes replicated to 3, 27, 60 or 100 resident scenes at a random table
+    depth (so every split-plane depth the launch picks, none included), random rays
+    from inside and around the domains, and rays generated from poses: against the
+    oracle."""
+    import torch
+
+    from navi_amd import scenes as S
+    from navi_amd.multiscene import ResidentScenes
+
+    rng = np.random.default_rng(5000 + seed)
+    makers = [lambda s, r: S.box_room(seed=s, resolution=r), lambda s, r: S.cluttered(seed=s, resolution=r),
+              lambda s, r: S.rooms(seed=s, resolution=r, grid=3)]
+    base = []
+    for _ in range(3):
+        sc = makers[int(rng.integers(0, 3))](int(rng.integers(0, 10_000)), int(rng.choice([32, 64, 128])))
+        words = sc.compile()
+        scale = float(rng.choice([1.0, 0.37, 3.3]))
+        shift = rng.uniform(-50, 50, 3)
+        lo = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_min_list, shift)]
+        hi = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_max, shift)]
+        base.append((words, lo, hi))
+    n = int(rng.choice([3, 27, 60, 100]))
+    scenes = [base[i % 3] for i in range(n)]
+    res = ResidentScenes(scenes, table_depth=int(rng.integers(4, 8)))
+    words = [s[0] for s in scenes]
+    bounds = [s[1] + s[2] for s in scenes]
+    n_env = 12
+    env_scene = rng.integers(0, n, n_env).astype(np.int32)
+    lo = np.array([scenes[s][1] for s in env_scene], np.float64)
+    hi = np.array([scenes[s][2] for s in env_scene], np.float64)
+    span = hi - lo
+    o = rng.uniform(lo[:, None, :] - 0.1 * span[:, None, :], hi[:, None, :] + 0.1 * span[:, None, :],
+                    (n_env, 256, 3)).astype(np.float32)
+    d = rng.normal(size=(n_env, 256, 3))
+    d[:, :20, 2] = 0.0  # some rays parallel to the z planes
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    max_steps = int(rng.integers(1, 300))
+    max_distance = float(np.float32(rng.uniform(1.0, 60.0)))
+    label = f"n{n}/depth{res.table_depth}"
+    ref = _oracle_multi(words, bounds, env_scene, o, d, max_steps, max_distance)
+    _compare(_run(res, env_scene, o, d, max_steps, max_distance), ref, max_distance, label)
+
+    # rays from poses: each env's first origin, a yawed 16 x 8 canonical table
+    pos = np.ascontiguousarray(o[:, 0, :])
+    yaw = rng.uniform(0, 2 * math.pi, n_env).astype(np.float32)
+    rot = np.stack([np.cos(yaw), np.sin(yaw)], 1).astype(np.float32)
+    local = oracle.ray_directions(16, 8)
+    c, s = rot[:, None, 0:1], rot[:, None, 1:2]
+    x, y, z = local[None, :, 0:1], local[None, :, 1:2], local[None, :, 2:3]
+    dirs = np.ascontiguousarray(np.concatenate(
+        [x * c + z * s, np.broadcast_to(y, (n_env,) + y.shape[1:]), (-x) * s + z * c], -1), np.float32)
+    origins = np.ascontiguousarray(np.broadcast_to(pos[:, None, :], dirs.shape))
+    ref = _oracle_multi(words, bounds, env_scene, origins, dirs, max_steps, max_distance)
+    dev = res.device
+    out_d = torch.full((n_env, 128), -7.0, device=dev)
+    out_s = torch.full((n_env, 128), -7, device=dev, dtype=torch.int32)
+    out_n = torch.full((n_env, 128), -7, device=dev, dtype=torch.int32)
+    res.cast_rays_poses(torch.from_numpy(env_scene).to(dev), torch.from_numpy(local).to(dev),
+                        torch.from_numpy(pos).to(dev), torch.from_numpy(rot).to(dev), out_d, out_s, max_steps,
+                        max_distance, out_steps=out_n, elevation_bins=8)
+    torch.cuda.synchronize()
+    _compare((out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), None), ref, max_distance,
+             label + "/poses")
