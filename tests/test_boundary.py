@@ -360,3 +360,22 @@ def test_relayout_resolves_bad_children_of_shallow_scenes(n, kept):
     assert bool((rec == 0x7FFFFFFE).any()) == (not kept)
     table = _native.root_table(rec, root)
     assert not ((table & 0xFFFFFFFF) == 0x7FFFFFFD).any()
+
+
+@pytest.mark.parametrize("header", sorted(p.name for p in (ROOT / "include").glob("*.h")))
+@pytest.mark.parametrize("lang", ["c", "c++"])
+def test_headers_compile_on_their_own(tmp_path, header, lang):
+    """The C ABI headers are self-contained plain C99 (and valid C++17), so a binding
+    written in C, cgo or C++ can include them alone."""
+    import shutil
+    import subprocess
+
+    compiler = {"c": "gcc", "c++": "g++"}[lang]
+    if shutil.which(compiler) is None:
+        pytest.skip(f"needs {compiler}")
+    src = tmp_path / ("h.c" if lang == "c" else "h.cpp")
+    src.write_text(f'#include "{header}"\nint main(void) {{ return 0; }}\n')
+    std = "-std=c99" if lang == "c" else "-std=c++17"
+    out = subprocess.run([compiler, std, "-Wall", "-Wextra", "-pedantic", "-Werror", "-fsyntax-only",
+                          "-I", str(ROOT / "include"), str(src)], capture_output=True, text=True)
+    assert out.returncode == 0, out.stderr
