@@ -158,9 +158,13 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 // P_n = hi of the n = 2^P depth-P cells and a pad float, the scene's block
 // rounded up to 16 bytes. A launch stages the deepest P (at most 6, at most
 // two levels above the cell table) whose scene table and planes fit kPlaneLds
-// bytes, else none: 22 KiB keeps seven 256-thread workgroups (7 waves per
-// SIMD) within a CU's 160 KiB of LDS.
+// bytes (seven 256-thread workgroups, 7 waves per SIMD, within a CU's 160 KiB
+// of LDS); failing that, the deepest that fits kPlaneLdsWide (five
+// workgroups): measured, planes at 6 or 5 waves per SIMD beat none at 7 (90
+// scenes: 13%, 110: 5%), a deeper P at 6 waves loses to a shallower one at 7,
+// and planes at 4 waves lose to none.
 constexpr size_t kPlaneLds = 22528;
+constexpr size_t kPlaneLdsWide = 32512;
 __host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
 __host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) { return (4u + 3u * axis_stride(depth) + 3u) & ~3u; }
 
@@ -763,14 +767,18 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     P.queue = queue_for(stream);
     constexpr int kThreads = 256;
     // Split planes of the deepest P <= min(D, 6), at most two levels above the
-    // table, whose LDS (with the scene table) fits kPlaneLds; none if no P does.
+    // table, whose LDS (with the scene table) fits kPlaneLds, else kPlaneLdsWide;
+    // none if no P does.
     const uint32_t D = P.cell_depth;
     int pd = 0;
-    for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p) {
-        if (static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= kPlaneLds) {
-            pd = p;
-            break;
+    for (const size_t budget : {kPlaneLds, kPlaneLdsWide}) {
+        for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p) {
+            if (static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) {
+                pd = p;
+                break;
+            }
         }
+        if (pd) break;
     }
     const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (pd ? scene_stride(pd) * sizeof(float) : 0));
     const bool poses = P.local_dirs != nullptr;

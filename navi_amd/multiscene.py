@@ -31,9 +31,11 @@ from . import _native
 
 
 # The tracer stages each scene's split planes in LDS when the scene table and
-# planes of a launch fit in this many bytes (kPlaneLds in trace_relaid.hip):
+# planes of a launch fit in this many bytes (kPlaneLds in trace_relaid.hip:
+# 7 waves per SIMD), else in the wider budget (kPlaneLdsWide: 5 waves):
 # 32 bytes per scene plus scene_stride(P) floats, P the planes' depth.
 PLANE_LDS_BYTES = 22528
+PLANE_LDS_BYTES_WIDE = 32512
 
 
 def _plane_bytes(depth: int) -> int:
@@ -43,10 +45,12 @@ def _plane_bytes(depth: int) -> int:
 def plane_depth(n_scenes: int, table_depth: int) -> int:
     """The split-plane depth the tracer uses for ``n_scenes`` scenes and cell tables of
     ``table_depth`` (launch_relaid in trace_relaid.hip): the deepest P <= min(D, 6), at
-    most two levels above the tables, whose planes fit ``PLANE_LDS_BYTES``; 0 for none."""
-    for p in range(min(table_depth, 6), max(4, table_depth - 2) - 1, -1):
-        if n_scenes * (32 + _plane_bytes(p)) <= PLANE_LDS_BYTES:
-            return p
+    most two levels above the tables, whose planes fit ``PLANE_LDS_BYTES``, else
+    ``PLANE_LDS_BYTES_WIDE``; 0 for none."""
+    for budget in (PLANE_LDS_BYTES, PLANE_LDS_BYTES_WIDE):
+        for p in range(min(table_depth, 6), max(4, table_depth - 2) - 1, -1):
+            if n_scenes * (32 + _plane_bytes(p)) <= budget:
+                return p
     return 0
 
 

@@ -262,16 +262,16 @@ def test_relaid_descent_limit_chains(gpu, corpus):
 
 
 def test_relaid_many_scenes_and_narrow_domains(gpu, corpus):
-    """100 resident scenes (more than the launch keeps split planes for in LDS),
+    """120 resident scenes (more than the launch keeps split planes for in LDS),
     and domains too narrow for their magnitude (float split planes collapse),
     both located by in-register splits instead of the plane lookup."""
     from navi_amd.multiscene import ResidentScenes, plane_depth
 
-    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(100)]
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(120)]
     res = ResidentScenes(many)
-    assert res.table_depth == 6 and plane_depth(100, 6) == 0
+    assert res.table_depth == 6 and plane_depth(120, 6) == 0
     env_scene, o, d = _rays(corpus, 24, 16, 16, seed=31)
-    env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 100
+    env_scene = (env_scene + 4 * np.arange(24, dtype=np.int32)) % 120
     ref = _oracle_multi([s[0] for s in many], [list(s[1]) + list(s[2]) for s in many], env_scene, o, d, 128, 30.0)
     _compare(_run(res, env_scene, o, d, 128, 30.0, elevation_bins=16), ref, 30.0, "many")
 
@@ -325,7 +325,8 @@ def test_relaid_every_table_depth(gpu, corpus, depth):
     _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, f"depth{depth}/narrow")
 
 
-@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (30, 6, 5), (60, 5, 4), (60, 6, 4), (100, 5, 0)])
+@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (30, 6, 5), (60, 5, 4), (60, 6, 4), (100, 6, 4),
+                                            (120, 5, 0)])
 def test_relaid_tables_below_the_planes(gpu, corpus, n, depth, planes):
     """Many resident scenes: the launch stages split planes of fewer levels than
     the cell tables have (one or two levels below them come from splits in
@@ -521,7 +522,7 @@ def test_scene_order_follows_measured_cost(gpu, corpus):
 
 @pytest.mark.parametrize("seed", range(8))
 def test_relaid_random_scene_counts_and_depths(gpu, seed):
-    """Random scenes replicated to 3, 27, 60 or 100 resident scenes at a random table
+    """Random scenes replicated to 3, 27, 60, 100 or 120 resident scenes at a random table
     depth (so every split-plane depth the launch picks, none included), random rays
     from inside and around the domains, and rays generated from poses: against the
     oracle."""
@@ -542,7 +543,7 @@ def test_relaid_random_scene_counts_and_depths(gpu, seed):
         lo = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_min_list, shift)]
         hi = [float(np.float32(v * scale + sh)) for v, sh in zip(sc.bbox_max, shift)]
         base.append((words, lo, hi))
-    n = int(rng.choice([3, 27, 60, 100]))
+    n = int(rng.choice([3, 27, 60, 100, 120]))
     scenes = [base[i % 3] for i in range(n)]
     res = ResidentScenes(scenes, table_depth=int(rng.integers(4, 8)))
     words = [s[0] for s in scenes]

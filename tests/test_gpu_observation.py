@@ -94,7 +94,7 @@ def test_pose_rays_equal_explicit_rays(gpu, corpus, az, el, depth):
     assert np.array_equal(explicit[0].view(np.uint32), got[0].view(np.uint32))
 
 
-@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (60, 6, 4), (100, 5, 0)])
+@pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (60, 6, 4), (100, 6, 4), (120, 5, 0)])
 def test_pose_rays_with_planes_above_the_tables(gpu, corpus, n, depth, planes):
     """Rays from poses over many resident scenes, where the launch stages split planes
     one or two levels above the cell tables, or none: against the oracle."""
