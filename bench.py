@@ -1,22 +1,22 @@
 """Throughput of the batched .gmdag sphere tracer on one MI355X.
 
-Workload (default): 16 seeded procedural scenes compiled at 1024^3 and all
-resident on the GPU (8 cluttered volumes, 8 room grids; seeds 100..115),
-1024 envs each assigned a scene id by seed, 256 x 48 rays per env
-(12,582,912 rays per step), max 256 steps, max distance 30 m, hit epsilon 0.01.
-A "step" is one trace of every ray of the batch, inputs already in HBM.
+Headline workload: 16 seeded procedural scenes compiled at 1024^3 and all
+resident on the GPU (8 cluttered volumes, 8 room grids; seeds 100..115), 1024
+envs each assigned a scene id by seed, 256 x 48 rays per env (12,582,912 rays
+per step), max 256 steps, max distance 30 m, hit epsilon 0.01. A "step" is one
+trace of every ray of the batch, inputs already in HBM.
 
 Prints one JSON line: rays/s, the dominant kernel's roofline (algorithmic bytes
-per launch / HIP-event launch time vs the 8 TB/s HBM peak), the CPU oracle
-timed on a bounded sample on the host cores, and the parity of that sample.
+per launch / HIP-event launch time vs the 8 TB/s HBM peak), the CPU oracle timed
+on the host cores, and the parity of the timed kernel's outputs against it; the
+same columns for each smaller workload of the benchmark definition and for the
+observation step (navi_amd/workloads.py defines all of them).
 """
 
 from __future__ import annotations
 
 import argparse
-import concurrent.futures as cf
 import json
-import math
 import os
 import sys
 import time
@@ -28,16 +28,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
-AZ, EL = 256, 48
-
-
-def _cache_dir() -> Path | None:
-    d = os.environ.get("NAVI_SCENE_CACHE", str(ROOT / ".scene_cache"))
-    if d in ("", "0", "off"):
-        return None
-    p = Path(d)
-    p.mkdir(parents=True, exist_ok=True)
-    return p
+CPU_RUNS = 5  # timed oracle runs (after one warm-up); the median is reported
 
 
 def _cpu_model() -> str:
@@ -51,130 +42,243 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def build_corpus(seeds, resolution, threads_total):
-    from navi_amd import scenes as S
-
-    cache = _cache_dir()
-    corpus = [S.corpus_scene(int(s), resolution) for s in seeds]
-    per = max(1, threads_total // 4)
-
-    def work(sc_seed):
-        sc, seed = sc_seed
-        path = cache / f"{sc.name}_{seed}_{resolution}.npy" if cache else None
-        if path is not None and path.exists():
-            sc.words = np.load(path)
-        else:
-            sc.compile(threads=per)
-            if path is not None:
-                np.save(path, sc.words)
-        return sc
-
-    with cf.ThreadPoolExecutor(max_workers=4) as ex:
-        corpus = list(ex.map(work, zip(corpus, seeds)))
-    return corpus
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def make_rays(corpus, n_envs, seed=4):
-    from navi_amd import scenes as S
-
-    rng = np.random.default_rng(seed)
-    env_scene = rng.integers(0, len(corpus), n_envs).astype(np.int32)
-    yaw = rng.uniform(0.0, 2.0 * math.pi, n_envs)
-    origins = np.empty((n_envs, 3), np.float32)
-    for s in range(len(corpus)):
-        idx = np.flatnonzero(env_scene == s)
-        if idx.size:
-            origins[idx] = corpus[s].free_origins(rng, idx.size)
-    local = S.canonical_directions(AZ, EL)
-    return env_scene, origins, yaw, local
-
-
-def observation_steps(res, t_es, origins_env, yaw_env, E, args):
-    """The full observation step, repeated for seeded random-walk poses: trace rays
-    generated in the kernel from each env's pose, then one launch that packs the fp16
-    (env, 1, El, Az) depth, reduces per-env clearance / ratios / collision and answers 4
-    point-SDF queries per env (the proposed move and three probes jittered +-0.3 m). A
-    move is kept when the proposed point clears 0.15 m. Returns rays/s over the steps."""
+def time_launches(fn, launches: int, warmup: int):
+    """HIP events on the current stream around each of ``launches`` calls of ``fn`` (after
+    ``warmup`` untimed calls): per-launch times in ms."""
     import torch
 
-    from navi_amd import scenes as S
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(launches + 1)]
+    evs[0].record(stream)
+    for k in range(launches):
+        fn()
+        evs[k + 1].record(stream)
+    torch.cuda.synchronize()
+    return np.array([evs[k].elapsed_time(evs[k + 1]) for k in range(launches)])
 
-    dev = res.device
-    steps = args.obs_steps
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(5)
-    pos = torch.from_numpy(np.ascontiguousarray(origins_env, np.float32)).to(dev)
-    yaw = torch.from_numpy(np.asarray(yaw_env, np.float32)).to(dev)
-    local = torch.from_numpy(S.canonical_directions(AZ, EL)).to(dev)
-    dpos = torch.randn((steps, E, 3), generator=gen, device=dev) * 0.05
-    dyaw = torch.randn((steps, E), generator=gen, device=dev) * 0.1
-    jitter = torch.rand((steps, E, 3, 3), generator=gen, device=dev) * 0.6 - 0.3
-    pscene = t_es.repeat_interleave(4)
-    rot = torch.empty((E, 2), device=dev)
-    pts = torch.empty((E, 4, 3), device=dev)
-    R = AZ * EL
+
+def time_cpu(fn):
+    """One warm-up, then the median of CPU_RUNS timed calls (s); returns (median, last result)."""
+    out = fn()
+    times = []
+    for _ in range(CPU_RUNS):
+        t = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t)
+    return float(np.median(times)), out
+
+
+def parity(gd, gs, gn, ref, gw=None) -> dict:
+    """Mismatch counts of GPU outputs against the oracle's (distances compared bit for bit;
+    both NaN counts as equal)."""
+    both_nan = np.isnan(gd) & np.isnan(ref["distance"])
+    dd = np.where(both_nan, 0.0, np.abs(gd.astype(np.float64) - ref["distance"]))
+    out = {
+        "rays": int(gd.size),
+        "hit_mismatch": int(np.sum((gs != 0) != (ref["semantic"] != 0))),
+        "semantic_mismatch": int(np.sum(gs != ref["semantic"])),
+        "steps_mismatch": int(np.sum(gn != ref["steps"])),
+        "max_abs_dd": float(np.nanmax(dd)) if dd.size else 0.0,
+        "bit_exact_distance": int(np.sum((gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both_nan)),
+    }
+    if gw is not None:
+        out["words_mismatch"] = int(np.sum(gw.astype(np.uint64) != ref["words"]))
+    return out
+
+
+def roofline(alg_bytes: int, ms: float, kernel: str, traffic=None) -> dict:
+    achieved = alg_bytes / (ms / 1e3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
+            "algorithmic_bytes_per_launch": int(alg_bytes)}
+
+
+def single_scene_config(cfg, dev, threads):
+    """One smaller workload: the record-layout tracer timed per launch, the word-layout
+    counting launch for the algorithmic bytes, the oracle timed on the whole ray set, and
+    the parity of the timed kernel's outputs (one entry per hit epsilon)."""
+    import torch
+
+    import oracle
+    from navi_amd import workloads as W
+    from navi_amd.multiscene import ResidentScenes
+
+    sc = cfg.scene()
+    sc.compile(threads=threads)
+    res = ResidentScenes([(sc.words, sc.bbox_min_list, sc.bbox_max)], dev)
+    o_np, d_np = W.single_scene_rays(cfg, sc)
+    o = torch.from_numpy(o_np).to(dev)
+    d = torch.from_numpy(d_np).to(dev)
+    E, R = d_np.shape[:2]
+    es = torch.zeros(E, dtype=torch.int32, device=dev)
     out_d = torch.empty((E, R), device=dev)
     out_s = torch.empty((E, R), device=dev, dtype=torch.int32)
-    d16 = torch.empty((E, 1, EL, AZ), device=dev, dtype=torch.float16)
-    stats = torch.empty((E, 5), device=dev)
-    coll = torch.empty((E,), device=dev, dtype=torch.int32)
-    pd = torch.empty((4 * E,), device=dev)
-    ps = torch.empty((4 * E,), device=dev, dtype=torch.int32)
-    pk = torch.empty((4 * E,), device=dev, dtype=torch.int32)
+    out_n = torch.empty((E, R), device=dev, dtype=torch.int32)
+    out_w = torch.empty((E, R), device=dev, dtype=torch.int32)
+    out = []
+    for eps in cfg.hit_epsilons:
+        def launch():
+            res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps,
+                          elevation_bins=cfg.el)
 
-    def observe():
-        res.observe(out_d, AZ, EL, args.max_distance, out_depth_f16=d16, out_stats=stats, out_collision=coll,
-                    points=pts.view(-1, 3), point_scene=pscene, point_distances=pd, point_semantics=ps,
-                    point_kind=pk)
+        res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, out_words=out_w,
+                      kernel="raw")
+        torch.cuda.synchronize()
+        words = int(out_w.to(torch.int64).sum().item())
+        launches = time_launches(launch, 50, 10)
+        ms = float(np.median(launches))
+        # the timed kernel's own outputs, with its step counts
+        res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, out_steps=out_n,
+                      elevation_bins=cfg.el)
+        torch.cuda.synchronize()
+        t_cpu, ref = time_cpu(lambda: oracle.trace(sc.words, o_np, d_np, cfg.max_steps, W.MAX_DISTANCE,
+                                                   sc.bbox_min_list, sc.bbox_max, hit_epsilon=eps,
+                                                   threads=threads))
+        alg = E * R * (24 + 8) + 8 * words
+        out.append({
+            "workload": cfg.describe() + f", hit epsilon {eps:g}",
+            "rays": E * R,
+            "ms": round(ms, 4),
+            "launch_ms": {"median": round(ms, 4), "p10": round(float(np.percentile(launches, 10)), 4),
+                          "p90": round(float(np.percentile(launches, 90)), 4), "launches": int(launches.size)},
+            "rays_per_s": round(E * R / (ms / 1e3), 1),
+            "dag_words_per_ray": round(words / (E * R), 3),
+            "roofline": roofline(alg, ms, "trace_relaid_kernel"),
+            "cpu_baseline": {"value": round(E * R / t_cpu, 1), "unit": "rays/s", "cores": threads, "kind": "port",
+                             "sample": f"the whole ray set ({E * R} rays), median of {CPU_RUNS} runs "
+                                       f"after 1 warm-up"},
+            "parity": parity(out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), ref,
+                             out_w.cpu().numpy()),
+        })
+        _log(f"{out[-1]['workload']}: {ms:.4f} ms, parity {out[-1]['parity']}")
+    return out
 
-    def one(k):
-        torch.stack((torch.cos(yaw), torch.sin(yaw)), 1, out=rot)
-        res.cast_rays_poses(t_es, local, pos, rot, out_d, out_s, args.max_steps, args.max_distance,
-                            elevation_bins=EL)
-        pts[:, 0] = pos + dpos[k]
-        pts[:, 1:] = pos[:, None, :] + jitter[k]
-        observe()
-        keep = pd.view(E, 4)[:, 0] >= 0.15
-        pos.copy_(torch.where(keep[:, None], pts[:, 0], pos))
-        yaw.add_(dyaw[k])
 
-    one(0)  # warm-up (the poses then start from step 1's state)
+def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cpu_envs):
+    """The observation step, 128 seeded random-walk steps (navi_amd.workloads.ObservationWalk),
+    timed with HIP events; then the last step's trace, fp16 depth, statistics and point
+    queries against the oracle, and its algorithmic bytes from a counting launch."""
+    import torch
+
+    import oracle
+    from navi_amd import workloads as W
+
+    E, R = len(env_scene), W.AZ * W.EL
+    walk = W.ObservationWalk(res, env_scene, origins_env, yaw, args.obs_steps, max_steps=args.max_steps,
+                             max_distance=args.max_distance)
+    walk.step(0)  # warm-up (the poses then start from step 1's state)
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
+    stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for k in range(steps):
-        one(k)
+    for k in range(args.obs_steps):
+        walk.step(k)
     ev1.record(stream)
     torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1) / steps
-    moved = float((pd.view(E, 4)[:, 0] >= 0.15).float().mean().item())
-    ev0.record(stream)
-    for _ in range(20):
-        observe()
-    ev1.record(stream)
+    ms = ev0.elapsed_time(ev1) / args.obs_steps
+    moved = float((walk.pd.view(E, W.POINTS_PER_ENV)[:, 0] >= W.CLEARANCE).float().mean().item())
+    observe_ms = float(np.median(time_launches(walk.observe, 20, 3)))
+
+    # the final poses: trace and observe once more, then check against the oracle
+    walk.trace()
+    walk.observe()
     torch.cuda.synchronize()
-    ms_observe = ev0.elapsed_time(ev1) / 20
+    o_np, d_np = walk.explicit_rays()
+    t_o = torch.from_numpy(o_np).to(res.device)
+    t_d = torch.from_numpy(d_np).to(res.device)
+    t_es = walk.env_scene
+    out_w = torch.empty((E, R), device=res.device, dtype=torch.int32)
+    out_n = torch.empty((E, R), device=res.device, dtype=torch.int32)
+    cd = torch.empty((E, R), device=res.device)
+    cs = torch.empty((E, R), device=res.device, dtype=torch.int32)
+    res.cast_rays(t_es, t_o, t_d, cd, cs, args.max_steps, args.max_distance, out_words=out_w, kernel="raw")
+    res.cast_rays_poses(t_es, walk.local, walk.pos, walk.rot, cd, cs, args.max_steps, args.max_distance,
+                        out_steps=out_n, elevation_bins=W.EL)
+    torch.cuda.synchronize()
+    words = int(out_w.to(torch.int64).sum().item())
+    del t_o, t_d, cd, cs
+
+    pool, base, nw, bounds = W.corpus_oracle_inputs(corpus)
+    sample = _env_sample(env_scene, len(corpus), cpu_envs)
+    es_np = np.asarray(env_scene)[sample]
+    t_cpu, ref = time_cpu(lambda: oracle.trace_multi(pool, base, nw, bounds, es_np, o_np[sample], d_np[sample],
+                                                     args.max_steps, args.max_distance, threads=threads))
+    gd = walk.out_d.cpu().numpy()[sample]
+    trace_parity = parity(gd, walk.out_s.cpu().numpy()[sample], out_n.cpu().numpy()[sample], ref)
+    want = oracle.observe(ref["distance"], W.AZ, W.EL, args.max_distance)
+    got16 = walk.depth16.cpu().numpy()[sample]
+    stats = walk.stats.cpu().numpy()[sample]
+    pts = walk.pts.view(-1, 3).cpu().numpy()
+    pscene = walk.pscene.cpu().numpy()
+    pw_total, pq_mismatch = 0, 0
+    gpd, gps, gpk = walk.pd.cpu().numpy(), walk.ps.cpu().numpy(), walk.pk.cpu().numpy()
+    for s, c in enumerate(corpus):
+        idx = np.flatnonzero(pscene == s)
+        if idx.size == 0:
+            continue
+        q = oracle.point_query(c.words, pts[idx], c.bbox_min_list, c.bbox_max)
+        pw_total += int(q["words"].sum())
+        pq_mismatch += int(np.sum((gpd[idx].view(np.uint32) != q["distance"].view(np.uint32))
+                                  & ~(np.isnan(gpd[idx]) & np.isnan(q["distance"]))))
+        pq_mismatch += int(np.sum(gps[idx] != q["semantic"]) + np.sum(gpk[idx] != q["kind"]))
+    # depths lie in [0, 1]: the difference of their binary16 bit patterns counts ulps
+    depth_ulps = np.abs(got16.view(np.uint16).astype(np.int32) - want["depth16"].view(np.uint16).astype(np.int32))
+    n_pts = int(pts.shape[0])
+    alg = E * R * (24 + 8) + 8 * words + 2 * E * R + n_pts * (12 + 8) + 8 * pw_total
+    obs_alg = E * R * (4 + 2) + E * 5 * 4 + E * 4 + n_pts * (12 + 8) + 8 * pw_total
     return {
-        "workload": f"{E} envs x {AZ}x{EL} rays from poses, {steps} seeded random-walk steps "
+        "workload": f"{E} envs x {W.AZ}x{W.EL} rays from poses, {args.obs_steps} seeded random-walk steps "
                     f"(dpos ~ N(0, 0.05 m), dyaw ~ N(0, 0.1 rad), move kept if its point SDF >= 0.15 m), "
-                    f"fp16 (env, 1, {EL}, {AZ}) depth + per-env stats + {4 * E} point queries per step",
+                    f"fp16 (env, 1, {W.EL}, {W.AZ}) depth + per-env stats + {n_pts} point queries per step",
         "rays_per_s": round(E * R / (ms / 1e3), 1),
         "ms_per_step": round(ms, 4),
-        "observe_launch_ms": round(ms_observe, 4),
+        "observe_launch_ms": round(observe_ms, 4),
         "entry_points": ["navi_trace_relaid_poses", "navi_observe"],
         "last_step_moves_kept": round(moved, 4),
-        "mean_min_distance": round(float(stats[:, 0].mean().item()), 4),
+        "mean_min_distance": round(float(walk.stats[:, 0].mean().item()), 4),
+        "roofline": roofline(alg, ms, "trace_relaid_kernel + observation_kernel (whole step)"),
+        "observation_kernel_roofline": roofline(obs_alg, observe_ms, "observation_kernel"),
+        "cpu_baseline": {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
+                         "kind": "port",
+                         "sample": f"the last step's rays of {sample.size} envs (the first "
+                                   f"{max(1, cpu_envs // len(corpus))} of each scene), tracing only, median of "
+                                   f"{CPU_RUNS} runs after 1 warm-up"},
+        "parity": dict(trace_parity,
+                       depth16_max_ulp=int(depth_ulps.max()) if depth_ulps.size else 0,
+                       min_distance_mismatch=int(np.sum(stats[:, 0].view(np.uint32)
+                                                        != want["stats"][:, 0].view(np.uint32))),
+                       ratio_max_abs_diff=float(np.abs(stats[:, 1:] - want["stats"][:, 1:]).max()),
+                       point_queries=n_pts, point_query_mismatch=pq_mismatch),
     }
+
+
+def _env_sample(env_scene, n_scenes, cpu_envs):
+    """The first cpu_envs // n_scenes envs of each scene (all envs when cpu_envs >= E)."""
+    E = len(env_scene)
+    if cpu_envs >= E:
+        return np.arange(E)
+    per = max(1, cpu_envs // n_scenes)
+    sample = []
+    for s in range(n_scenes):
+        sample.extend(np.flatnonzero(np.asarray(env_scene) == s)[:per].tolist())
+    return np.array(sorted(sample))
 
 
 def dropin_timing(corpus, env_scene, t_o, t_d, args):
     """The drop-in torch_sdf.cast_rays on one resident DAG (scene 0) for the envs that use
-    it: record-layout tracer (converted once per DAG tensor) versus the word-layout kernel."""
+    it: record-layout tracer (prepared once per DAG tensor) versus the word-layout kernel."""
     import torch
 
     from navi_amd import torch_sdf
+    from navi_amd import workloads as W
 
     idx = torch.from_numpy(np.flatnonzero(env_scene == 0)).to(t_o.device)
     o = t_o.index_select(0, idx).contiguous()
@@ -184,22 +288,14 @@ def dropin_timing(corpus, env_scene, t_o, t_d, args):
     out_d = torch.empty(o.shape[:2], device=t_o.device)
     out_s = torch.empty(o.shape[:2], device=t_o.device, dtype=torch.int32)
     result = {"envs": int(idx.numel()), "rays": int(o.shape[0] * o.shape[1]), "scene": sc.name}
+    t0 = time.perf_counter()
+    torch_sdf.prepare(dag, sc.bbox_min_list, list(sc.bbox_max))
+    result["prepare_s"] = round(time.perf_counter() - t0, 3)
     for kernel, reps in (("auto", 10), ("raw", 2)):
         def call():
             torch_sdf.cast_rays(dag, o, d, out_d, out_s, args.max_steps, args.max_distance, sc.bbox_min_list,
-                                list(sc.bbox_max), args.resolution, True, elevation_bins=EL, kernel=kernel)
-        t0 = time.perf_counter()
-        call()  # auto: converts the DAG once
-        torch.cuda.synchronize()
-        first = time.perf_counter() - t0
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record()
-        for _ in range(reps):
-            call()
-        ev1.record()
-        torch.cuda.synchronize()
-        ms = ev0.elapsed_time(ev1) / reps
+                                list(sc.bbox_max), args.resolution, True, elevation_bins=W.EL, kernel=kernel)
+        ms = float(np.mean(time_launches(call, reps, 1)))
         # host wall time per call with a synchronize after each (Python checks included)
         t0 = time.perf_counter()
         for _ in range(reps):
@@ -207,48 +303,8 @@ def dropin_timing(corpus, env_scene, t_o, t_d, args):
             torch.cuda.synchronize()
         wall_ms = (time.perf_counter() - t0) / reps * 1e3
         result[kernel] = {"rays_per_s": round(result["rays"] / (ms / 1e3), 1), "ms": round(ms, 3),
-                          "wall_ms": round(wall_ms, 3), "first_call_s": round(first, 3)}
+                          "wall_ms": round(wall_ms, 3)}
     return result
-
-
-def small_configs(dev):
-    """The smaller workloads of the benchmark definition, on the record-layout tracer:
-    they are latency-bound (too few rays to fill the chip), reported as ms per launch."""
-    import torch
-
-    from navi_amd import scenes as S
-    from navi_amd.multiscene import ResidentScenes
-
-    cases = [("1 env x 64x16 rays, box room @64^3, max 64 steps", S.box_room(seed=1, resolution=64), 1, 64, 16, 64),
-             ("4 envs x 256x48 rays, cluttered @128^3, max 128 steps", S.cluttered(seed=2, resolution=128), 4, 256,
-              48, 128),
-             ("64 envs x 256x48 rays, rooms @512^3, max 256 steps", S.rooms(seed=3, resolution=512), 64, 256, 48,
-              256)]
-    out = []
-    for name, sc, envs, az, el, max_steps in cases:
-        sc.compile()
-        res = ResidentScenes([(sc.words, sc.bbox_min_list, sc.bbox_max)], dev, keep_words=False)
-        rng = np.random.default_rng(envs)
-        origins = sc.free_origins(rng, envs)
-        dirs = S.world_directions(S.canonical_directions(az, el), rng.uniform(0, 2 * math.pi, envs))
-        o = torch.from_numpy(np.ascontiguousarray(np.broadcast_to(origins[:, None, :], dirs.shape))).to(dev)
-        d = torch.from_numpy(np.ascontiguousarray(dirs)).to(dev)
-        es = torch.zeros(envs, dtype=torch.int32, device=dev)
-        out_d = torch.empty(o.shape[:2], device=dev)
-        out_s = torch.empty(o.shape[:2], device=dev, dtype=torch.int32)
-        for _ in range(3):
-            res.cast_rays(es, o, d, out_d, out_s, max_steps, 30.0, elevation_bins=el)
-        torch.cuda.synchronize()
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record()
-        for _ in range(20):
-            res.cast_rays(es, o, d, out_d, out_s, max_steps, 30.0, elevation_bins=el)
-        ev1.record()
-        torch.cuda.synchronize()
-        ms = ev0.elapsed_time(ev1) / 20
-        out.append({"workload": name, "ms": round(ms, 4), "rays_per_s": round(envs * az * el / (ms / 1e3), 1)})
-    return out
 
 
 def main() -> int:
@@ -263,8 +319,12 @@ def main() -> int:
     ap.add_argument("--max-distance", type=float, default=30.0)
     ap.add_argument("--cpu-envs", type=int, default=1024,
                     help="envs in the CPU-baseline sample (taken evenly over the scenes; all by default)")
+    ap.add_argument("--obs-cpu-envs", type=int, default=128,
+                    help="envs of the observation step's last step traced by the CPU baseline")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-raw", action="store_true", help="skip timing the reference-layout kernel")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time the headline workload only (no smaller workloads, observation step or drop-in)")
     ap.add_argument("--obs-steps", type=int, default=128,
                     help="observation-step workload: steps of seeded random-walk poses (0 to skip)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -282,19 +342,19 @@ def main() -> int:
     import torch
 
     import oracle
+    from navi_amd import scenes as S
+    from navi_amd import workloads as W
     from navi_amd.multiscene import ResidentScenes
 
     n_cpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     t0 = time.time()
     seeds = list(range(100, 100 + args.scenes))
-    corpus = build_corpus(seeds, args.resolution, n_cpu)
+    corpus = W.build_corpus(seeds, args.resolution, n_cpu, W.scene_cache_dir(ROOT))
     t_compile = time.time() - t0
-    print(f"[bench] compiled {len(corpus)} scenes @{args.resolution}^3 in {t_compile:.1f}s, "
-          f"{sum(c.words.size for c in corpus) * 8 / 1e6:.1f} MB of words", file=sys.stderr, flush=True)
+    _log(f"compiled {len(corpus)} scenes @{args.resolution}^3 in {t_compile:.1f}s, "
+         f"{sum(c.words.size for c in corpus) * 8 / 1e6:.1f} MB of words")
 
-    env_scene, origins_env, yaw, local = make_rays(corpus, args.envs)
-    from navi_amd import scenes as S
-
+    env_scene, origins_env, yaw, local = W.corpus_rays(corpus, args.envs)
     dirs = S.world_directions(local, yaw)
     origins = np.ascontiguousarray(np.broadcast_to(origins_env[:, None, :], dirs.shape))
 
@@ -319,7 +379,7 @@ def main() -> int:
 
     def step(kernel="relaid"):
         res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, kernel=kernel,
-                      elevation_bins=EL)
+                      elevation_bins=W.EL)
 
     def timed(kernel, steps, warmup):
         for _ in range(warmup):
@@ -335,90 +395,55 @@ def main() -> int:
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / steps
 
-    # untimed: counts of words the reference algorithm loads, and step counts
-    res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_steps=out_n,
-                  out_words=out_w)
+    # untimed: counts of words the reference algorithm loads (word-layout counting kernel)
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_words=out_w, kernel="raw")
     torch.cuda.synchronize()
     total_words = int(out_w.to(torch.int64).sum().item())
-    mean_steps = float(out_n.float().mean().item())
-    hit_rate = float((out_s != 0).float().mean().item())
-
-    def per_launch(steps):
-        """Each launch between its own events (after the bracketed run): the spread."""
-        stream = torch.cuda.current_stream(dev)
-        evs = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-        evs[0].record(stream)
-        for k in range(steps):
-            step("relaid")
-            evs[k + 1].record(stream)
-        torch.cuda.synchronize()
-        return np.array([evs[k].elapsed_time(evs[k + 1]) for k in range(steps)])
 
     ms_raw = timed("raw", max(1, args.steps // 4), 1) if not args.no_raw else None
     ms = timed("relaid", args.steps, args.warmup)
     rays_per_s = n_rays / (ms / 1e3)
-    launches = per_launch(args.steps)
+    launches = time_launches(step, args.steps, 0)
     launch_ms = {"median": round(float(np.median(launches)), 4), "p10": round(float(np.percentile(launches, 10)), 4),
                  "p90": round(float(np.percentile(launches, 90)), 4), "launches": int(launches.size)}
-
+    # the timed kernel's outputs of one more launch, with its own step counts
+    res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_steps=out_n,
+                  elevation_bins=W.EL)
+    torch.cuda.synchronize()
+    mean_steps = float(out_n.float().mean().item())
+    hit_rate = float((out_s != 0).float().mean().item())
     alg_bytes = n_rays * (24 + 8) + 8 * total_words
-    achieved_gbs = alg_bytes / (ms / 1e3) / 1e9
+    _log(f"headline: {ms:.4f} ms per step, {rays_per_s / 1e9:.3f} G rays/s")
 
-    # CPU baseline + parity on a bounded sample: the first env of each scene
     cpu = None
-    parity = None
+    par = None
     if not args.no_cpu:
-        if args.cpu_envs >= E:
-            sample = np.arange(E)
+        sample = _env_sample(env_scene, len(corpus), args.cpu_envs)
+        if sample.size == E:
             sample_text = f"the whole batch: {E} envs x {R} rays = {E * R} rays"
         else:
-            per = max(1, args.cpu_envs // len(corpus))
-            sample = []
-            for s in range(len(corpus)):
-                sample.extend(np.flatnonzero(env_scene == s)[:per].tolist())
-            sample = np.array(sorted(sample)[: max(args.cpu_envs, len(corpus))])
-            sample_text = (f"{sample.size} envs x {R} rays = {sample.size * R} rays (the first {per} envs "
-                           f"of each of the {len(corpus)} scenes)")
-        pool = np.concatenate([c.words for c in corpus])
-        base = np.cumsum([0] + [c.words.size for c in corpus[:-1]]).astype(np.uint64)
-        nw = np.array([c.words.size for c in corpus], np.uint64)
-        bounds = np.array([c.bbox_min_list + c.bbox_max for c in corpus], np.float32)
+            sample_text = (f"{sample.size} envs x {R} rays = {sample.size * R} rays (the first "
+                           f"{max(1, args.cpu_envs // len(corpus))} envs of each of the {len(corpus)} scenes)")
+        pool, base, nw, bounds = W.corpus_oracle_inputs(corpus)
         o_s, d_s, es_s = origins[sample], dirs[sample], env_scene[sample]
-        threads = n_cpu
-
-        def run_cpu():
-            return oracle.trace_multi(pool, base, nw, bounds, es_s, o_s, d_s, args.max_steps,
-                                      args.max_distance, threads=threads)
-
-        ref = run_cpu()  # warm-up
-        times = []
-        for _ in range(2):
-            t = time.perf_counter()
-            run_cpu()
-            times.append(time.perf_counter() - t)
-        t_cpu = float(np.median(times))
-        cpu = {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
+        t_cpu, ref = time_cpu(lambda: oracle.trace_multi(pool, base, nw, bounds, es_s, o_s, d_s, args.max_steps,
+                                                         args.max_distance, threads=n_cpu))
+        cpu = {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": n_cpu,
                "kind": "port", "cpu_model": _cpu_model(),
-               "sample": f"{sample_text}, median of 2 timed runs after 1 warm-up"}
-        gd = out_d.cpu().numpy()[sample]
-        gs = out_s.cpu().numpy()[sample]
-        gn = out_n.cpu().numpy()[sample]
-        gw = out_w.cpu().numpy()[sample]
-        both_nan = np.isnan(gd) & np.isnan(ref["distance"])
-        dd = np.where(both_nan, 0.0, np.abs(gd.astype(np.float64) - ref["distance"]))
-        parity = {
-            "rays": int(gd.size),
-            "hit_mismatch": int(np.sum((gs != 0) != (ref["semantic"] != 0))),
-            "semantic_mismatch": int(np.sum(gs != ref["semantic"])),
-            "steps_mismatch": int(np.sum(gn != ref["steps"])),
-            "words_mismatch": int(np.sum(gw.astype(np.uint64) != ref["words"])),
-            "max_abs_dd": float(np.nanmax(dd)),
-            "bit_exact_distance": int(np.sum((gd.view(np.uint32) == ref["distance"].view(np.uint32)) | both_nan)),
-        }
+               "sample": f"{sample_text}, median of {CPU_RUNS} timed runs after 1 warm-up"}
+        par = parity(out_d.cpu().numpy()[sample], out_s.cpu().numpy()[sample], out_n.cpu().numpy()[sample], ref,
+                     out_w.cpu().numpy()[sample])
+        _log(f"headline parity {par}")
 
-    obs = observation_steps(res, t_es, origins_env, yaw, E, args) if args.obs_steps > 0 else None
-    dropin = dropin_timing(corpus, env_scene, t_o, t_d, args) if args.obs_steps > 0 else None
-    small = small_configs(dev) if args.obs_steps > 0 else None
+    small = obs = dropin = None
+    if not args.headline_only:
+        small = []
+        for cfg in W.SMALL_CONFIGS:
+            small.extend(single_scene_config(cfg, dev, n_cpu))
+        if args.obs_steps > 0:
+            obs = observation_walk(res, corpus, env_scene, origins_env, yaw, args, n_cpu, args.obs_cpu_envs)
+            _log(f"observation step: {obs['ms_per_step']} ms, parity {obs['parity']}")
+        dropin = dropin_timing(corpus, env_scene, t_o, t_d, args)
 
     traffic = None
     tp = Path(args.traffic_profile)
@@ -443,7 +468,7 @@ def main() -> int:
         "data": "synthetic (seeded procedural scenes and poses)",
         "config": {
             "workload": f"{len(corpus)} resident scenes @{args.resolution}^3 (seeds {seeds[0]}..{seeds[-1]}), "
-                        f"{E} envs x {AZ}x{EL} rays, max {args.max_steps} steps, max {args.max_distance} m",
+                        f"{E} envs x {W.AZ}x{W.EL} rays, max {args.max_steps} steps, max {args.max_distance} m",
             "envs": E, "rays_per_env": R, "rays_per_step": n_rays, "scenes": len(corpus),
             "resolution": args.resolution, "max_steps": args.max_steps,
             "max_distance": args.max_distance, "hit_epsilon": 0.01,
@@ -453,21 +478,12 @@ def main() -> int:
             "mean_steps_per_ray": round(mean_steps, 3), "hit_rate": round(hit_rate, 4),
             "dag_words_per_ray": round(total_words / n_rays, 3),
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(achieved_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "kernel": "trace_relaid_kernel",
-            "algorithmic_bytes_per_launch": alg_bytes,
-        },
+        "roofline": roofline(alg_bytes, ms, "trace_relaid_kernel", traffic),
         "cpu_baseline": cpu,
-        "parity": parity,
+        "parity": par,
+        "small_configs": small,
         "observation_step": obs,
         "dropin_cast_rays": dropin,
-        "small_configs": small,
         "scene_compile_s": round(t_compile, 2),
     }
     print(json.dumps(line), flush=True)

@@ -2,10 +2,14 @@
  * navi_trace.h — C ABI of the MI355X .gmdag sphere tracer (libnavi_trace.so).
  *
  * Plain pointers and sizes only: every device pointer is a HIP device address,
- * `stream` is a hipStream_t passed as void* (NULL = the null stream). All
- * entry points are asynchronous with respect to the host, allocate nothing on
- * the call path, and return 0 on success or a negative NAVI_E* code; the
- * message of the last failure on the calling thread is navi_last_error().
+ * `stream` is a hipStream_t passed as void* (NULL = the null stream). The
+ * tracing, query and post-pass entry points are asynchronous with respect to
+ * the host and return 0 on success or a negative NAVI_E* code; the message of
+ * the last failure on the calling thread is navi_last_error(). They allocate
+ * nothing and never wait for the device once navi_device_init has run on the
+ * current device (the record-layout tracers call it themselves on their first
+ * launch on a device that lacks it). The host-memory helpers (navi_relayout,
+ * navi_record_depth, navi_build_cell_table) run synchronously on the CPU.
  *
  * Reference interfaces (paths relative to the seismael/navi checkout) are cited
  * on each entry point.
@@ -23,7 +27,17 @@ extern "C" {
 #define NAVI_E_ARG (-1)     /* invalid argument (message says which) */
 #define NAVI_E_LAUNCH (-2)  /* HIP launch or runtime failure */
 #define NAVI_E_LAYOUT (-3)  /* DAG cannot be re-laid (see navi_scene_build) */
-#define NAVI_E_NOMEM (-4)   /* device allocation failed (scene build only) */
+#define NAVI_E_NOMEM (-4)   /* device allocation failed (navi_device_init) */
+
+/*
+ * Per-device set-up (no reference counterpart: the reference kernel keeps no
+ * state between launches, kernel.cu:311-326). On the current device,
+ * allocates and clears the record-layout tracers' work-queue counters (32 KiB,
+ * kept until the process ends); idempotent and thread-safe. Call it where
+ * allocation and a device wait are acceptable (scene load), so that no later
+ * launch on this device allocates or waits.
+ */
+int navi_device_init(void);
 
 /* Hit threshold of the reference tracer (projects/torch-sdf/cpp_src/kernel.cuh:7). */
 #define NAVI_DEFAULT_HIT_EPSILON 0.01f

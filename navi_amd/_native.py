@@ -36,6 +36,9 @@ _lib.navi_last_error.argtypes = []
 _lib.navi_version.restype = ctypes.c_char_p
 _lib.navi_version.argtypes = []
 
+_lib.navi_device_init.restype = ctypes.c_int
+_lib.navi_device_init.argtypes = []
+
 _lib.navi_cast_rays.restype = ctypes.c_int
 _lib.navi_cast_rays.argtypes = [
     _vp, ctypes.c_uint64, _vp, _vp, _vp, _vp, ctypes.c_int64, ctypes.c_int32, ctypes.c_float,
@@ -174,6 +177,24 @@ def check(code: int) -> None:
     """Raise ``RuntimeError`` (the exception type TORCH_CHECK surfaces) for a failed call."""
     if code != NAVI_OK:
         raise RuntimeError(last_error() or f"navi_trace call failed with code {code}")
+
+
+_initialised: set[int] = set()
+
+
+def device_init(device) -> None:
+    """``navi_device_init`` on ``device`` (a CUDA ``torch.device`` or index), once per
+    process: the tracers' work-queue counters, so that no launch allocates or waits."""
+    import torch
+
+    index = torch.device(device).index if not isinstance(device, int) else device
+    if index is None:
+        index = torch.cuda.current_device()
+    if index in _initialised:
+        return
+    with torch.cuda.device(index):
+        check(_lib.navi_device_init())
+    _initialised.add(index)
 
 
 def float3(values) -> ctypes.Array:

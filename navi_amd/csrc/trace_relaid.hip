@@ -6,9 +6,10 @@
 // Execution model (CDNA4, wave64):
 //   * persistent waves: the grid holds as many workgroups as the chip keeps
 //     resident; waves claim work units (128 rays = two 8 x 8 tiles, or one
-//     tile for batches too small to fill the chip) from a per-stream counter
-//     pair, the last wave rearming it; without a counter (more than 256
-//     streams) wave w takes 64-ray chunks w, w + W, ...;
+//     tile for batches too small to fill the chip) from a counter pair of
+//     the launch's stream (or of the graph node it was captured into), the
+//     last wave rearming it; without a counter (all 4096 pairs in use) wave
+//     w takes 64-ray chunks w, w + W, ...;
 //   * lane refill: once 8 of 64 lanes have finished their rays, the idle lanes
 //     take the next rays (ballot + mbcnt rank), so a wave never idles on a few
 //     long rays;
@@ -41,6 +42,7 @@
 #include <cmath>
 #include <map>
 #include <mutex>
+#include <thread>
 #include <unordered_map>
 #include <utility>
 
@@ -592,11 +594,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // resource's bound only keeps a corrupt caller-built pool inside its
         // allocation (a read past it returns 0).
         if (shallow) {
-            while (descending) {
+            // A shallow scene's slots all lie at depth <= 31, at most 31 - D
+            // reads below the table; the wave-uniform bound of 32 - D trips
+            // only matters for a pool whose max_depth understates it (a cycle
+            // behind a zeroed descriptor), which then ends like the 32-level
+            // limit (stale result) instead of looping.
+            for (uint32_t trip = D; descending && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
                 slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
                 cur_rec = slot;  // read again only while internal
                 descending = slot < kSlotBadChild;
             }
+            descending = false;
         } else {
             while (descending) {
                 slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
@@ -723,42 +731,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
 // Resident waves the chip holds for this kernel: the persistent grid is sized
 // to exactly that, so no wave waits for a slot and the sweep has no second,
 // partly empty round.
-// (per LDS size of the launch; guarded by g_queue_mu).
-std::map<std::pair<int, size_t>, int> g_grid_blocks;
+// (per device, kernel variant and LDS size of the launch; guarded by g_queue_mu).
+std::map<std::pair<std::pair<int, int>, size_t>, int> g_grid_blocks;
 
-// Work-queue counters, one pair per (device, stream), allocated once per device
-// at its first launch (a 2 KiB device buffer, zeroed then). Launches on one
-// stream run in order, so a pair is never used by two launches at once; the
-// kernel's last wave rearms it. Streams beyond kQueueSlots use the static schedule.
-constexpr int kQueueSlots = 256;
+// Work-queue counters: pairs [next unit, finished waves] in one 32 KiB device
+// buffer per device, allocated and zeroed by navi_device_init. An eager launch
+// uses the pair of its (stream, thread for hipStreamPerThread): launches on one
+// stream run in order, so the pair is never used by two launches at once, and
+// the kernel's last wave rearms it for the next. A launch recorded into a graph
+// gets a pair of its own, never shared: a graph may be replayed on any stream,
+// and two launches of one capture may run concurrently; replays of one graph
+// run in order and each rearms the pair. Launches find no pair (and take the
+// static schedule) once kQueueSlots are in use, or while a stream captures on a
+// device that was never initialised (no allocation inside a capture).
+constexpr int kQueueSlots = 4096;
 std::mutex g_queue_mu;
-std::unordered_map<int, uint32_t*> g_queue_mem;
-std::map<std::pair<int, void*>, int> g_queue_slot;
+struct DeviceQueues {
+    uint32_t* mem = nullptr;
+    int used = 0;
+    std::map<std::pair<void*, size_t>, int> slot;  // (stream, thread) -> pair
+};
+std::unordered_map<int, DeviceQueues> g_queues;
+
+// Allocates the current device's counters if it has none (g_queue_mu held).
+int init_device_locked(int dev) {
+    DeviceQueues& q = g_queues[dev];
+    if (q.mem != nullptr) return NAVI_OK;
+    void* p = nullptr;
+    if (hipMalloc(&p, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess)
+        return set_error(NAVI_E_NOMEM, "work-queue counters: hipMalloc failed on device %d", dev);
+    if (hipMemset(p, 0, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        (void)hipFree(p);
+        return set_error(NAVI_E_LAUNCH, "work-queue counters: clearing failed on device %d", dev);
+    }
+    q.mem = static_cast<uint32_t*>(p);
+    return NAVI_OK;
+}
 
 uint32_t* queue_for(hipStream_t stream) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess) status = hipStreamCaptureStatusNone;
+    const bool capturing = status != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> lock(g_queue_mu);
-    uint32_t*& mem = g_queue_mem[dev];
-    if (mem == nullptr) {
-        void* p = nullptr;
-        if (hipMalloc(&p, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess) return nullptr;
-        if (hipMemset(p, 0, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess) {
-            (void)hipFree(p);
-            return nullptr;
-        }
-        mem = static_cast<uint32_t*>(p);
+    DeviceQueues& q = g_queues[dev];
+    if (q.mem == nullptr && (capturing || init_device_locked(dev) != NAVI_OK)) return nullptr;
+    if (capturing) return q.used < kQueueSlots ? q.mem + 2 * q.used++ : nullptr;
+    const size_t thread = stream == hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
+    const auto key = std::make_pair(static_cast<void*>(stream), thread);
+    auto it = q.slot.find(key);
+    if (it == q.slot.end()) {
+        if (q.used >= kQueueSlots) return nullptr;
+        it = q.slot.emplace(key, q.used++).first;
     }
-    const auto key = std::make_pair(dev, static_cast<void*>(stream));
-    auto it = g_queue_slot.find(key);
-    if (it == g_queue_slot.end()) {
-        int used = 0;
-        for (const auto& kv : g_queue_slot)
-            if (kv.first.first == dev) ++used;
-        if (used >= kQueueSlots) return nullptr;
-        it = g_queue_slot.emplace(key, used).first;
-    }
-    return mem + 2 * it->second;
+    return q.mem + 2 * it->second;
 }
 
 int launch_relaid(RelaidParams P, hipStream_t stream) {
@@ -796,7 +824,9 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
         default: kernel = NAVI_RELAID(0, 0); break;
     }
 #undef NAVI_RELAID
-    const auto key = std::make_pair(2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses), lds);
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const auto key = std::make_pair(std::make_pair(dev, 2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses)), lds);
     int grid_blocks = 0;
     {
         std::lock_guard<std::mutex> lock(g_queue_mu);
@@ -804,9 +834,8 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
         if (it != g_grid_blocks.end()) grid_blocks = it->second;
     }
     if (grid_blocks == 0) {
-        int dev = 0, cus = 0, per_cu = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        int cus = 0, per_cu = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
             per_cu = 4;
@@ -847,12 +876,13 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     if (!cell_tables) return set_error(NAVI_E_ARG, "cell_tables is required (navi_build_cell_table)");
     if (table_depth < 4 || table_depth > 7) return set_error(NAVI_E_ARG, "table_depth must be in [4, 7]");
     if (n_scenes > kMaxScenes) return set_error(NAVI_E_ARG, "navi_trace_relaid takes at most 1024 scenes");
-    // 32-bit slot addressing: record * 8 + octant must fit in uint32
-    if (n_records > (1ull << 27)) return set_error(NAVI_E_ARG, "record pool exceeds 2^27 records (4 GiB)");
-    const int64_t n_rays = n_envs * rays_per_env;
-    // 32-bit work indexing: every ray index times 3 must fit in uint32
-    if (n_rays > 0x3fffffffLL || rays_per_env > 0x3fffffffLL)
+    // the pool is read through a buffer resource whose size field (bytes) is
+    // 32-bit: 2^27 records would wrap it to 0
+    if (n_records >= (1ull << 27)) return set_error(NAVI_E_ARG, "record pool must hold fewer than 2^27 records (4 GiB)");
+    if (rays_per_env > (1LL << 30) || (rays_per_env > 0 && n_envs > (1LL << 30) / rays_per_env))
         return set_error(NAVI_E_ARG, "navi_trace_relaid handles at most 2^30 rays per launch");
+    // 32-bit work indexing: every ray index times 3, plus 2, fits in uint32
+    const int64_t n_rays = n_envs * rays_per_env;
     if (n_rays > 0 && (!out_distances || !out_semantics))
         return set_error(NAVI_E_ARG, "output pointers must be non-null");
     P = RelaidParams{};
@@ -882,6 +912,15 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
 }
 
 }  // namespace navi
+
+extern "C" int navi_device_init(void) {
+    using namespace navi;
+    int dev = 0;
+    const hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "no HIP device: %s", hipGetErrorString(err));
+    std::lock_guard<std::mutex> lock(g_queue_mu);
+    return init_device_locked(dev);
+}
 
 extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
                                  int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth,

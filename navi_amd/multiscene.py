@@ -131,7 +131,9 @@ class ResidentScenes:
             recs.append(rec)
             roff += rec.shape[0]
         if self.relaid_ok:
-            if roff > (1 << 27):  # navi_trace_relaid reads the pool through a 4 GiB buffer resource
+            # navi_trace_relaid reads the pool through a buffer resource whose
+            # 32-bit byte size must not wrap: fewer than 2^27 records
+            if roff >= (1 << 27):
                 self.relaid_ok = False
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
@@ -157,8 +159,24 @@ class ResidentScenes:
         self.order_by_cost = bool(order_by_cost) and self.n_scenes > 1
         self.scene_cost: np.ndarray | None = None  # mean steps per ray, once measured
         self._scene_rank: torch.Tensor | None = None  # [n_scenes + 1] position of each scene; unknown ids last
-        self._cost_pending: tuple[Any, torch.Tensor] | None = None  # (event, pinned [2, n_scenes + 1])
+        self._cost_pending = False  # a measurement is queued behind _cost_event
         self._cost_version = 0
+        # Everything a launch needs is allocated here, at scene load: the
+        # tracer's work-queue counters, and the buffers of the cost measurement
+        # and its readback. A launch then allocates nothing and never waits
+        # (the measuring launch aside, which takes a steps buffer when the
+        # caller passes none, and launches that sort envs for a new env_scene).
+        cuda = self.device.type == "cuda"
+        n1 = self.n_scenes + 1
+        self._cost_dev = torch.zeros((2, n1), dtype=torch.int64, device=self.device)
+        self._cost_host = torch.zeros((2, n1), dtype=torch.int64, pin_memory=cuda)
+        self._rank_host = torch.zeros(n1, dtype=torch.int64, pin_memory=cuda)
+        self._rank_dev = torch.zeros(n1, dtype=torch.int64, device=self.device)
+        self._cost_event = None
+        if cuda:
+            _native.device_init(self.device)
+            with torch.cuda.device(self.device):
+                self._cost_event = torch.cuda.Event()
 
     @property
     def pool_bytes(self) -> int:
@@ -183,10 +201,14 @@ class ResidentScenes:
             self._order_key = key
         return self._order
 
+    def _capturing(self) -> bool:
+        return self.device.type == "cuda" and torch.cuda.is_current_stream_capturing()
+
     def _cost_steps(self, out_steps: Any, e: int, r: int, sort_by_scene: bool) -> tuple[Any, bool]:
-        """The steps tensor for a launch and whether the launch measures the scenes' costs."""
+        """The steps tensor for a launch and whether the launch measures the scenes' costs
+        (never inside a graph capture: its readback belongs to one eager launch)."""
         if (not (self.order_by_cost and sort_by_scene) or self.scene_cost is not None
-                or self._cost_pending is not None or e * r == 0):
+                or self._cost_pending or e * r == 0 or self._capturing()):
             return out_steps, False
         if out_steps is None:
             out_steps = torch.empty((e, r), dtype=torch.int32, device=self.device)
@@ -198,22 +220,22 @@ class ResidentScenes:
         n = self.n_scenes
         with torch.cuda.device(self.device):
             idx = torch.where((env_scene >= 0) & (env_scene < n), env_scene, n).to(torch.int64)
-            sums = torch.zeros(n + 1, dtype=torch.int64, device=self.device)
-            sums.index_add_(0, idx, steps.sum(dim=1, dtype=torch.int64))
-            rays = torch.bincount(idx, minlength=n + 1) * int(steps.shape[1])
-            host = torch.empty((2, n + 1), dtype=torch.int64, pin_memory=True)
-            host[0].copy_(sums, non_blocking=True)
-            host[1].copy_(rays, non_blocking=True)
-            event = torch.cuda.Event()
-            event.record()
-        self._cost_pending = (event, host)
+            self._cost_dev.zero_()
+            self._cost_dev[0].index_add_(0, idx, steps.sum(dim=1, dtype=torch.int64))
+            self._cost_dev[1].index_add_(0, idx, torch.full_like(idx, int(steps.shape[1])))
+            self._cost_host.copy_(self._cost_dev, non_blocking=True)
+            self._cost_event.record()
+        self._cost_pending = True
 
     def _poll_cost(self) -> None:
-        """Adopt the measured scene costs if their copy has completed (never waits)."""
-        if self._cost_pending is None or not self._cost_pending[0].query():
+        """Adopt the measured scene costs if their copy has completed (never waits; never
+        inside a graph capture, where an event query is not allowed)."""
+        if not self._cost_pending or self._capturing():
             return
-        host = self._cost_pending[1].numpy()
-        self._cost_pending = None
+        if self._cost_event is not None and not self._cost_event.query():
+            return
+        host = self._cost_host.numpy()
+        self._cost_pending = False
         n = self.n_scenes
         sums, rays = host[0, :n].astype(np.float64), host[1, :n]
         if not np.any(rays > 0):  # no ray of a known scene: measure on a later launch
@@ -225,7 +247,14 @@ class ResidentScenes:
         rank[np.argsort(-cost, kind="stable")] = np.arange(n)
         rank[n] = n
         self.scene_cost = cost
-        self._scene_rank = torch.from_numpy(rank).to(self.device)
+        # written once: the pinned source of the asynchronous copy is never reused
+        self._rank_host.copy_(torch.from_numpy(rank))
+        if self.device.type == "cuda":
+            with torch.cuda.device(self.device):
+                self._rank_dev.copy_(self._rank_host, non_blocking=True)
+        else:
+            self._rank_dev.copy_(self._rank_host)
+        self._scene_rank = self._rank_dev
         self._cost_version += 1
 
     def cast_rays(self, env_scene: torch.Tensor, origins: torch.Tensor, dirs: torch.Tensor,

@@ -5,6 +5,6 @@
 (``SdfDagBackend``, the env CLI, tests) import it unchanged.
 """
 
-from .backend import cast_rays
+from .backend import cast_rays, invalidate, prepare
 
 __all__ = ["cast_rays"]

@@ -181,3 +181,21 @@ def cast_rays(
         skip_direction_validation,
         **extra,
     )
+
+
+def prepare(dag_tensor: torch.Tensor, bbox_min: list[float], bbox_max: list[float]) -> bool:
+    """Scene-load step (an extension; the reference converts nothing): builds the
+    record-layout copy of ``dag_tensor`` that ``cast_rays(kernel="auto")`` traces, so
+    the calls that follow neither copy, allocate nor wait. See
+    :func:`navi_amd.torch_sdf_backend.prepare`."""
+    if not HAS_CUDA_BACKEND or torch_sdf_backend is None:
+        raise RuntimeError("torch_sdf_backend is not available. Build the HIP tracer library "
+                           "(navi_amd/_lib/libnavi_trace.so) first.")
+    return torch_sdf_backend.prepare(dag_tensor, bbox_min, bbox_max)
+
+
+def invalidate(dag_tensor: torch.Tensor | None = None) -> None:
+    """Drop the record-layout copy of ``dag_tensor`` (all copies when None); needed
+    after writes that bypass its version counter (``.data``, raw pointers)."""
+    if HAS_CUDA_BACKEND and torch_sdf_backend is not None:
+        torch_sdf_backend.invalidate(dag_tensor)

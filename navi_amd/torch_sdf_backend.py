@@ -16,13 +16,20 @@ Additions, all keyword-only so the positional contract is unchanged:
 traced in angular tiles) and ``kernel``.
 
 Kernels. ``kernel="auto"`` (default) traces with the record-layout tracer
-(``navi_trace_relaid``): the first call with a given DAG tensor copies its words
-to the host once, converts them (``navi_relayout``, ``navi_build_cell_table``)
-and keeps the device copy, keyed by the tensor object, its version counter
-(in-place writes invalidate it) and the bbox. DAGs the record layout cannot
-hold (a leaf semantic above 0x7fff) and batches above 2^30 rays use the
-word-layout kernel (``navi_cast_rays``), as does ``kernel="raw"``. Results are
-identical either way.
+(``navi_trace_relaid``) over a record-layout copy of the DAG tensor: its words
+copied to the host once, converted (``navi_relayout``, ``navi_build_cell_table``)
+and uploaded, keyed by the tensor object, its version counter (in-place tensor
+ops invalidate it), its address and the bbox. ``prepare(dag_tensor, bbox_min,
+bbox_max)`` does that at scene load (the reference's ``_load_scene``,
+``sdfdag_backend.py:1893-1900``); otherwise the first ``cast_rays`` with the
+tensor does it, with a device-to-host copy that waits for the device. Writes
+that bypass the version counter (through ``.data``, or from outside PyTorch)
+need ``invalidate(dag_tensor)``. DAGs the record layout cannot hold (a leaf
+semantic above 0x7fff) and batches above 2^30 rays use the word-layout kernel
+(``navi_cast_rays``), as does ``kernel="raw"``. Results are identical either
+way. Once prepared, a call with ``skip_direction_validation=True`` allocates
+nothing and never waits for the device, as the reference's
+(``bindings.cpp:91-109``).
 """
 
 from __future__ import annotations
@@ -41,8 +48,9 @@ from . import _native
 _DIRECTION_NORM_EPS = 1e-4  # kernel.cuh:9
 HIT_EPSILON = 0.01  # kernel.cuh:7
 _INT32_MAX = 0x7FFFFFFF
+RELAID_MAX_RAYS = 1 << 30  # rays per navi_trace_relaid launch; larger batches take navi_cast_rays
 
-__all__ = ["cast_rays", "HIT_EPSILON"]
+__all__ = ["cast_rays", "prepare", "invalidate", "HIT_EPSILON"]
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -163,6 +171,30 @@ def _record_layout(dag_tensor: torch.Tensor, bbox_min, bbox_max):
         return entry.scenes
 
 
+def prepare(dag_tensor: torch.Tensor, bbox_min, bbox_max) -> bool:
+    """Convert ``dag_tensor`` (int64 words on a CUDA device) to the record layout now,
+    so that ``cast_rays`` calls with it neither copy, allocate nor wait. Synchronous.
+    Returns whether the record layout holds the DAG (else ``kernel="auto"`` traces it
+    with the word-layout kernel, which needs no preparation)."""
+    _check(dag_tensor.is_cuda, "dag_tensor must be a CUDA tensor")
+    _check(dag_tensor.dtype == torch.int64, "dag_tensor must be int64")
+    _check(dag_tensor.is_contiguous(), "dag_tensor must be contiguous")
+    _validate_bounds(bbox_min, bbox_max)
+    _native.device_init(dag_tensor.device)
+    return _record_layout(dag_tensor, bbox_min, bbox_max) is not None
+
+
+def invalidate(dag_tensor: torch.Tensor | None = None) -> None:
+    """Drop the record-layout copy of ``dag_tensor`` (of every tensor when None). In-place
+    tensor ops bump the version counter and need no call; writes through ``.data`` or a
+    raw pointer do."""
+    with _layout_lock:
+        if dag_tensor is None:
+            _layouts.clear()
+        else:
+            _layouts.pop(id(dag_tensor), None)
+
+
 def cast_rays(
     dag_tensor: torch.Tensor,
     origins: torch.Tensor,
@@ -196,7 +228,8 @@ def cast_rays(
     n_envs, rays = int(origins.size(0)), int(origins.size(1))
     n_rays = n_envs * rays
     dev = dag_tensor.device
-    scenes = _record_layout(dag_tensor, bbox_min, bbox_max) if kernel == "auto" and n_rays <= (1 << 30) else None
+    scenes = (_record_layout(dag_tensor, bbox_min, bbox_max)
+              if kernel == "auto" and n_rays <= RELAID_MAX_RAYS else None)
     if scenes is not None:
         with torch.cuda.device(dev):
             stream = torch.cuda.current_stream(dev).cuda_stream

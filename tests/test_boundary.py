@@ -166,6 +166,16 @@ def test_c_abi_rejects_bad_arguments_without_a_gpu():
     code = lib.navi_trace_relaid(1, 1, 1, 1, 1, 6, None, None, 1 << 20, 1 << 20, 0, 1, 1, 1, 1, 4, 1.0, 0.01,
                                   None, None)
     assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
+    # one ray past the limit the drop-in's kernel choice uses, and a product that overflows int64
+    over = torch_sdf_backend.RELAID_MAX_RAYS + 1
+    for envs, rays in ((over, 1), (1, over), (1 << 62, 4)):
+        code = lib.navi_trace_relaid(1, 1, 1, 1, 1, 6, None, None, envs, rays, 0, 1, 1, 1, 1, 4, 1.0, 0.01,
+                                      None, None)
+        assert code == _native.NAVI_E_ARG and "2^30" in _native.last_error()
+    # 2^27 records would wrap the 32-bit byte size of the pool's buffer resource to 0
+    code = lib.navi_trace_relaid(1, 1 << 27, 1, 1, 1, 6, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None,
+                                  None)
+    assert code == _native.NAVI_E_ARG and "2^27" in _native.last_error()
     code = lib.navi_trace_relaid(1, 1, 1, 1, None, 6, None, None, 4, 4, 0, 1, 1, 1, 1, 4, 1.0, 0.01, None, None)
     assert code == _native.NAVI_E_ARG and "cell_tables" in _native.last_error()
     for depth in (3, 8):

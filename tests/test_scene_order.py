@@ -47,10 +47,11 @@ def test_costs_become_the_env_order():
     # step sums and ray counts per scene (the last column collects unknown ids);
     # scene 3 has the most steps per ray, scene 1 none measured (gets the mean)
     host = torch.tensor([[300, 0, 500, 2000, 77], [100, 0, 100, 400, 9]], dtype=torch.int64)
-    res._cost_pending = (_Pending(), host)
+    res._cost_host.copy_(host)
+    res._cost_pending, res._cost_event = True, _Pending()
     res._poll_cost()
     assert res.scene_cost is None  # the copy has not completed: nothing changes
-    res._cost_pending = (_Done(), host)
+    res._cost_event = _Done()
     res._poll_cost()
     want = np.array([3.0, (3.0 + 5.0 + 5.0) / 3, 5.0, 5.0])
     assert np.allclose(res.scene_cost, want, rtol=0, atol=1e-12)
@@ -83,7 +84,7 @@ def test_measurement_uses_the_callers_steps_once():
     assert steps is mine and measure
     steps, measure = res._cost_steps(None, 2, 8, False)  # unsorted launches never measure
     assert steps is None and not measure
-    res._cost_pending = (_Pending(), torch.zeros((2, 3), dtype=torch.int64))
+    res._cost_pending, res._cost_event = True, _Pending()
     steps, measure = res._cost_steps(None, 2, 8, True)  # one measurement at a time
     assert steps is None and not measure
 
@@ -94,9 +95,10 @@ def test_empty_measurements_are_retried():
     res = ResidentScenes(_scenes(2), "cpu")
     assert res._cost_steps(None, 0, 8, True) == (None, False)  # empty batches measure nothing
     # only unknown scene ids (last column) were traced: nothing adopted, measured again later
-    res._cost_pending = (_Done(), torch.tensor([[0, 0, 50], [0, 0, 10]], dtype=torch.int64))
+    res._cost_host.copy_(torch.tensor([[0, 0, 50], [0, 0, 10]], dtype=torch.int64))
+    res._cost_pending, res._cost_event = True, _Done()
     res._poll_cost()
-    assert res.scene_cost is None and res._cost_pending is None
+    assert res.scene_cost is None and not res._cost_pending
     steps, measure = res._cost_steps(None, 2, 8, True)
     assert measure and tuple(steps.shape) == (2, 8)
 
