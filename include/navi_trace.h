@@ -33,9 +33,10 @@ extern "C" {
  * Per-device set-up (no reference counterpart: the reference kernel keeps no
  * state between launches, kernel.cu:311-326). On the current device,
  * allocates and clears the record-layout tracers' work-queue counters (32 KiB,
- * kept until the process ends); idempotent and thread-safe. Call it where
- * allocation and a device wait are acceptable (scene load), so that no later
- * launch on this device allocates or waits.
+ * kept until the process ends) and looks up the device's copy of
+ * navi_trace_relaid_noalloc's static scratch; idempotent and thread-safe. Call
+ * it where allocation and a device wait are acceptable (scene load), so that
+ * no later launch on this device allocates or waits.
  */
 int navi_device_init(void);
 
@@ -180,6 +181,28 @@ int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_re
                       const float* dirs, float* out_distances, int32_t* out_semantics,
                       int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                       void* stream);
+
+/*
+ * navi_trace_relaid for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. Same arguments and results as
+ * navi_trace_relaid; it calls no hipMalloc, hipFree or allocating routine at
+ * any time, not even on its first call on a device. Its work-queue counter
+ * pair lives in a static device array of 256 bytes (each GPU the library runs
+ * on holds its copy until the process ends), cleared by a small kernel on
+ * `stream` before every launch; a launch needs one pair whatever its size, so
+ * the limits are navi_trace_relaid's (at most 2^30 rays, fewer than 2^27
+ * records). Every call on one GPU shares that pair: calls that overlap on one
+ * GPU (concurrent streams, or graph replays running at once) race and may
+ * leave rays unwritten; serialise them, or use navi_trace_relaid.
+ */
+int navi_trace_relaid_noalloc(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
+                              int32_t n_scenes, const uint64_t* cell_tables, int32_t table_depth,
+                              const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
+                              int64_t rays_per_env, int32_t elevation_bins, const float* origins,
+                              const float* dirs, float* out_distances, int32_t* out_semantics,
+                              int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
+                              void* stream);
 
 /*
  * navi_trace_relaid with the rays generated in the kernel from per-env poses

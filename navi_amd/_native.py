@@ -66,6 +66,9 @@ _lib.navi_trace_relaid.argtypes = [
     ctypes.c_int32, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
 
+_lib.navi_trace_relaid_noalloc.restype = ctypes.c_int
+_lib.navi_trace_relaid_noalloc.argtypes = _lib.navi_trace_relaid.argtypes
+
 _lib.navi_trace_relaid_poses.restype = ctypes.c_int
 _lib.navi_trace_relaid_poses.argtypes = [
     _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64,

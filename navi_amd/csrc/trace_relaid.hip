@@ -789,10 +789,49 @@ uint32_t* queue_for(hipStream_t stream) {
     return q.mem + 2 * it->second;
 }
 
-int launch_relaid(RelaidParams P, hipStream_t stream) {
+// Scratch of navi_trace_relaid_noalloc: one work-queue counter pair per device
+// in a static device array (each GPU the library runs on holds its own copy
+// until the process ends). Host code never uses the array's name as an
+// address: navi_device_init (or the entry point's first call on a device)
+// looks up the device's copy with hipGetSymbolAddress and keeps the pointer.
+constexpr int kScratchWords = 64;  // 256 bytes; a launch uses words 0 and 1
+constexpr int kMaxDevices = 64;
+uint32_t* g_scratch_ptr[kMaxDevices] = {};  // guarded by g_queue_mu
+
+}  // namespace navi
+
+static __device__ __align__(256) uint32_t scratch[navi::kScratchWords];
+
+namespace navi {
+
+// The current device's copy of `scratch` into *out (g_queue_mu held; dev current).
+int scratch_locked(int dev, uint32_t** out) {
+    if (dev < 0 || dev >= kMaxDevices)
+        return set_error(NAVI_E_ARG, "device %d is beyond the %d devices the scratch table holds", dev, kMaxDevices);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || ptr == nullptr)
+            return set_error(NAVI_E_LAUNCH, "scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                             hipGetErrorString(err));
+        g_scratch_ptr[dev] = static_cast<uint32_t*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return NAVI_OK;
+}
+
+// Zeroes the counter pair before a launch that shares it (a kernel node, never a
+// memset node, so the launch can be captured into a graph).
+__global__ void clear_queue_kernel(uint32_t* queue) {
+    if (threadIdx.x < 2) queue[threadIdx.x] = 0u;
+}
+
+// queue: the counter pair to use (no_alloc), or null to take the stream's pair.
+int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = nullptr) {
+    const bool no_alloc = scratch_queue != nullptr;
     P.n_chunks = (P.n_rays + 63u) / 64u;
     P.unit_rays = kUnitRays;
-    P.queue = queue_for(stream);
+    P.queue = no_alloc ? scratch_queue : queue_for(stream);
     constexpr int kThreads = 256;
     // Split planes of the deepest P <= min(D, 6), at most two levels above the
     // table, whose LDS (with the scene table) fits kPlaneLds, else kPlaneLdsWide;
@@ -840,8 +879,10 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
             per_cu = 4;
         grid_blocks = cus * per_cu;
-        std::lock_guard<std::mutex> lock(g_queue_mu);
-        g_grid_blocks[key] = grid_blocks;
+        if (!no_alloc) {  // the no-allocation entry point keeps no host table entry either
+            std::lock_guard<std::mutex> lock(g_queue_mu);
+            g_grid_blocks[key] = grid_blocks;
+        }
     }
     // Small batches: one-tile units, so that more waves get work (a launch
     // wants several units per resident wave to balance the long rays).
@@ -851,6 +892,7 @@ int launch_relaid(RelaidParams P, hipStream_t stream) {
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
     if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;
+    if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
@@ -919,7 +961,39 @@ extern "C" int navi_device_init(void) {
     const hipError_t err = hipGetDevice(&dev);
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "no HIP device: %s", hipGetErrorString(err));
     std::lock_guard<std::mutex> lock(g_queue_mu);
+    uint32_t* ptr = nullptr;
+    const int code = scratch_locked(dev, &ptr);
+    if (code != NAVI_OK) return code;
     return init_device_locked(dev);
+}
+
+extern "C" int navi_trace_relaid_noalloc(const uint32_t* records, uint64_t n_records,
+                                         const navi_relaid_scene* scenes, int32_t n_scenes,
+                                         const uint64_t* cell_tables, int32_t table_depth,
+                                         const int32_t* env_scene, const int32_t* env_order, int64_t n_envs,
+                                         int64_t rays_per_env, int32_t elevation_bins, const float* origins,
+                                         const float* dirs, float* out_distances, int32_t* out_semantics,
+                                         int32_t max_steps, float max_distance, float hit_epsilon,
+                                         int32_t* out_steps, void* stream) {
+    using namespace navi;
+    RelaidParams P;
+    const int code = relaid_setup(P, records, n_records, scenes, n_scenes, cell_tables, table_depth, env_scene,
+                                  env_order, n_envs, rays_per_env, elevation_bins, out_distances, out_semantics,
+                                  max_steps, max_distance, hit_epsilon, out_steps);
+    if (code != NAVI_OK || P.n_rays == 0) return code;
+    if (!origins || !dirs) return set_error(NAVI_E_ARG, "ray and output pointers must be non-null");
+    P.origins = origins;
+    P.dirs = dirs;
+    int dev = 0;
+    const hipError_t err = hipGetDevice(&dev);
+    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "no HIP device: %s", hipGetErrorString(err));
+    uint32_t* queue = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        const int sc = scratch_locked(dev, &queue);
+        if (sc != NAVI_OK) return sc;
+    }
+    return launch_relaid(P, static_cast<hipStream_t>(stream), queue);
 }
 
 extern "C" int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_relaid_scene* scenes,
