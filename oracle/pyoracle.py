@@ -12,8 +12,13 @@ Functions and what pins each one (the pinning tests in brackets, ``tests/<file>:
   [::test_unit_box_rays_within_reference_tolerance] and a cache-free brute-force march
   [::test_cache_free_march_agrees_off_faces]; a planted mistake must fail them
   [::test_planted_mistake_is_caught].
-* ``point_query`` — build-defined clearance query (no reference kernel), pinned against a
-  pure-Python descent and closed forms [test_oracle_tracer::test_point_query_matches_python_descent].
+* ``point_query`` — build-defined clearance query (no reference kernel). Pinned by answers
+  derived by hand on the reference's fixture DAGs (outside / faces / popcount child choice /
+  void octants) [test_oracle_tracer::test_point_query_closed_forms], by the pinned tracer's
+  first step at the same point (leaf distance, 1000 outside, void side = sum of the +x and
+  -x exits) [::test_point_query_agrees_with_one_step_trace], and by the compiler's pruning
+  guarantee on the dense grid (every sample of a void block exceeds the bound; the parent's
+  side, a planted mistake, violates it) [::test_point_query_void_bound_holds_on_the_grid].
 * ``half_to_float`` / ``float_to_half`` — IEEE binary16, pinned exhaustively against numpy's
   float16 [test_oracle_codecs::test_half_decode_exhaustive, ::test_half_encode_rne_matches_numpy].
   ``float_to_half(quirk=True)`` restates ``projects/voxel-dag/src/compiler.cpp:542-560``, pinned by

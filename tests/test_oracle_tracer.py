@@ -202,34 +202,124 @@ def test_invariants_and_thread_independence():
     assert (r1["steps"] <= 64).all()
 
 
-def test_point_query_matches_python_descent():
-    scene = sf.room_with_spheres(res=32, seed=6, n_spheres=6)
+def _case(name):
+    return next(c for c in CASES if c["name"] == name)
+
+
+def _half(bits):
+    return float(np.array([bits], np.uint16).view(np.float16)[0])
+
+
+def test_point_query_closed_forms():
+    """Answers derived by hand on the reference's own fixture DAGs
+    (test_sphere_tracing.py:783-877,926-949): outside the box (1000, 0, kind 0), the
+    faces themselves inside (inclusive test, kernel.cu:108-112); a pruned octant is a
+    void of side 0.5 (bound 0.5 * 1.7321, kind 2); present octants are their leaves'
+    fp16 distance and semantic (kind 1), the child chosen by popcount of the lower mask
+    bits (kernel.cu:192-198)."""
+    box = ([0.0, 0.0, 0.0], [1.0, 1.0, 1.0])
+    octants = np.array([[0.25 + 0.5 * (k & 1), 0.25 + 0.5 * ((k >> 1) & 1), 0.25 + 0.5 * (k >> 2)]
+                        for k in range(8)], np.float32)
+    # octant_selection: all eight octants present, leaf k has semantic k + 1, distance 0x1d1f
+    r = oracle.point_query(_words(_case("octant_selection")), octants, *box)
+    assert r["kind"].tolist() == [1] * 8 and r["semantic"].tolist() == list(range(1, 9))
+    assert (r["distance"] == np.float32(_half(0x1D1F))).all()
+    # void_macro_cells: only octant 7 present (mask 0x80), its leaf semantic 0x11
+    r = oracle.point_query(_words(_case("void_macro_cells")), octants, *box)
+    assert r["kind"].tolist() == [2] * 7 + [1]
+    assert (r["distance"][:7] == np.float32(0.5 * 1.7321)).all() and (r["semantic"][:7] == 0).all()
+    assert r["semantic"][7] == 0x11 and r["distance"][7] == np.float32(_half(0x1D1F))
+    # sparse_mask_popcount: top byte 0x25, so bits 62..55 hold mask 0x4a = octants 1, 3, 6
+    # -> child slots 0, 1, 2 (semantics 11, 33, 66)
+    r = oracle.point_query(_words(_case("sparse_mask_popcount")), octants, *box)
+    assert r["kind"].tolist() == [2, 1, 2, 1, 2, 2, 1, 2]
+    assert r["semantic"].tolist() == [0, 11, 0, 33, 0, 0, 66, 0]
+    # outside the box by a hair on each side, far outside, and on the faces
+    words = _words(_case("octant_selection"))
+    eps = np.float32(1e-6)
+    out = []
+    for a in range(3):
+        for v in (np.float32(0) - eps, np.float32(1) + eps, np.float32(-50), np.float32(50)):
+            q = np.full(3, 0.5, np.float32)
+            q[a] = v
+            out.append(q)
+    r = oracle.point_query(words, np.array(out), *box)
+    assert (r["kind"] == 0).all() and (r["distance"] == 1000.0).all() and (r["semantic"] == 0).all()
+    faces = np.array([[0, 0, 0], [1, 1, 1], [1, 0, 0.25], [0.5, 1, 0.5]], np.float32)
+    r = oracle.point_query(words, faces, *box)
+    assert (r["kind"] == 1).all()
+    # the >= rule: on a midplane the upper octant is taken (kernel.cu:165-176)
+    assert r["semantic"].tolist() == [1, 8, 2, 8]
+
+
+def _query_scene():
+    # truncation 2 m so that void octants of 1, 2 and 4 voxels occur (bound 1.7321 * side)
+    scene = sf.room_with_spheres(res=64, seed=6, n_spheres=10, trunc=2.0)
     words = oracle.compile_dense(scene["grid"], scene["voxel"])
-    rng = np.random.default_rng(1)
-    pts = rng.uniform(np.array(scene["bmin"]) - 1, np.array(scene["bmax"]) + 1, (500, 3)).astype(np.float32)
-    r = oracle.point_query(words, pts, scene["bmin"], scene["bmax"])
-    lo0 = np.array(scene["bmin"], np.float32)
-    hi0 = np.array(scene["bmax"], np.float32)
-    for i, p in enumerate(pts):
-        if not ((p >= lo0).all() and (p <= hi0).all()):
-            assert r["kind"][i] == 0 and r["distance"][i] == 1000.0
+    rng = np.random.default_rng(3)
+    lo = np.array(scene["bmin"], np.float32)
+    hi = np.array(scene["bmax"], np.float32)
+    pts = rng.uniform(lo - 0.5, hi + 0.5, (6000, 3)).astype(np.float32)
+    return scene, words, pts
+
+
+def test_point_query_agrees_with_one_step_trace():
+    """The pinned tracer (known answers of test_sphere_tracing.py) at max_steps = 1 starts
+    with the same fresh descent as a point query: outside the box it reports 1000; at a
+    leaf its distance t = 0 + d is the leaf's distance (or a hit at t = 0); in a void cell
+    the exits along +x and -x add up to the cell's side, which the query's bound divided
+    by 1.7321 must equal (both cell sides are one float subtraction from exact)."""
+    scene, words, pts = _query_scene()
+    q = oracle.point_query(words, pts, scene["bmin"], scene["bmax"])
+    assert {0, 1, 2} <= set(q["kind"].tolist())
+
+    def one_step(direction):
+        d = np.broadcast_to(np.array(direction, np.float32), pts.shape)
+        return oracle.trace(words, pts, d, 1, 3000.0, scene["bmin"], scene["bmax"])
+
+    px, mx = one_step([1, 0, 0]), one_step([-1, 0, 0])
+    out = q["kind"] == 0
+    assert (px["distance"][out] == 1000.0).all()
+    leaf = q["kind"] == 1
+    hit = leaf & (q["semantic"] != 0) & (q["distance"] < oracle.HIT_EPSILON)
+    assert np.array_equal(px["distance"][leaf & ~hit], q["distance"][leaf & ~hit])
+    assert (px["semantic"][leaf & ~hit] == 0).all()
+    assert (px["distance"][hit] == 0.0).all() and np.array_equal(px["semantic"][hit], q["semantic"][hit])
+    void = q["kind"] == 2
+    side = px["distance"][void].astype(np.float64) + mx["distance"][void]
+    bound_side = q["distance"][void].astype(np.float64) / np.float32(1.7321)
+    assert void.sum() > 100
+    assert np.allclose(side, bound_side, rtol=1e-5, atol=2e-5)
+    assert set(np.round(bound_side / scene["voxel"]).astype(int).tolist()) == {1, 2, 4}
+
+
+def _void_bound_violations(scene, words, pts, scale):
+    """Void points whose returned bound (times ``scale``) is not below every grid sample
+    of their void block: the compiler prunes an octant only when its smallest sample
+    exceeds 1.7321 x its side (compiler.cpp:626,639-643)."""
+    q = oracle.point_query(words, pts, scene["bmin"], scene["bmax"])
+    grid, voxel = scene["grid"], scene["voxel"]
+    bmin = np.array(scene["bmin"], np.float64)
+    bad = checked = 0
+    for i in np.flatnonzero(q["kind"] == 2):
+        bound = float(q["distance"][i]) * scale
+        half = int(round(float(q["distance"][i]) / 1.7321 / voxel))
+        u = (pts[i].astype(np.float64) - bmin) / voxel / half
+        if np.any(np.abs(u - np.round(u)) < 1e-4):  # too close to a block face to place it
             continue
-        lo, hi = lo0.copy(), hi0.copy()
-        node = 0
-        while True:
-            w = int(words[node])
-            if w >> 63:
-                assert r["kind"][i] == 1 and r["semantic"][i] == (w >> 16) & 0xFFFF
-                assert r["distance"][i] == np.array([w & 0xFFFF], np.uint16).view(np.float16)[0]
-                break
-            mid = ((lo + hi) * np.float32(0.5)).astype(np.float32)
-            ge = p >= mid
-            octant = int(ge[0]) | (int(ge[1]) << 1) | (int(ge[2]) << 2)
-            lo = np.where(ge, mid, lo)
-            hi = np.where(ge, hi, mid)
-            mask = (w >> 55) & 0xFF
-            if not (mask >> octant) & 1:
-                assert r["kind"][i] == 2
-                assert r["distance"][i] == np.float32((hi[0] - lo[0]) * np.float32(1.7321))
-                break
-            node = int(words[(w & 0xFFFFFFFF) + bin(mask & ((1 << octant) - 1)).count("1")]) & 0xFFFFFFFF
+        x0, y0, z0 = (np.floor(u).astype(int) * half).tolist()
+        block = grid[z0:z0 + half, y0:y0 + half, x0:x0 + half]
+        checked += 1
+        bad += int(float(block.min()) < bound * (1.0 - 1e-5))
+    return bad, checked
+
+
+def test_point_query_void_bound_holds_on_the_grid():
+    """Every void point's bound lies below every sample of its block in the dense grid
+    the DAG was compiled from (the compiler's pruning rule, compiler.cpp:626,639-643);
+    the parent's side, a plausible mistake, breaks it."""
+    scene, words, pts = _query_scene()
+    bad, checked = _void_bound_violations(scene, words, pts, 1.0)
+    assert checked > 100 and bad == 0
+    bad, checked = _void_bound_violations(scene, words, pts, 2.0)
+    assert bad > 0
