@@ -124,8 +124,15 @@ typedef struct navi_relaid_scene {
     float bbox_max[3];
     uint32_t max_depth;   /* navi_record_depth of the scene's records as navi_relayout wrote
                              them; 0xffffffff if unknown */
-    uint32_t reserved;    /* 0 */
+    uint32_t flags;       /* NAVI_SCENE_* bits; 0 when unknown */
 } navi_relaid_scene;
+
+/* navi_relaid_scene.flags: no leaf slot of the scene's records (nor an inlined
+ * root leaf) has its fp16 sign bit set, so distances never decrease along a
+ * ray. When every scene of a launch has it (and its boxes are below 2^100),
+ * the tracer skips the reference's void cache (kernel.cu:265-267), which then
+ * only repeats what a fresh query finds. */
+#define NAVI_SCENE_NONNEG_LEAVES 1u
 
 /*
  * Depth of a scene's record graph (no reference counterpart; host memory):

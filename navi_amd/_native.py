@@ -104,7 +104,19 @@ _lib.navi_observe.argtypes = [ctypes.POINTER(Observation), ctypes.POINTER(PointQ
 # Layout of navi_relaid_scene (include/navi_trace.h), 48 bytes.
 RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot", "<u4"),
                       ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,)), ("max_depth", "<u4"),
-                      ("reserved", "<u4")]
+                      ("flags", "<u4")]
+SCENE_NONNEG_LEAVES = 1  # navi_relaid_scene.flags bit (include/navi_trace.h)
+
+
+def nonneg_leaves(records, root_slot) -> bool:
+    """Whether no leaf slot of ``records`` (uint32 [n, 8]) nor an inlined root leaf has
+    its fp16 sign bit set (``NAVI_SCENE_NONNEG_LEAVES``)."""
+    import numpy as np
+
+    rec = np.asarray(records, dtype=np.uint32)
+    leaf_neg = (rec >> np.uint32(31)).astype(bool) & ((rec >> np.uint32(15)) & np.uint32(1)).astype(bool)
+    root = int(root_slot)
+    return not bool(leaf_neg.any()) and not (root >> 31 and (root >> 15) & 1)
 
 
 def relayout(words):

@@ -156,9 +156,10 @@ struct SceneLds {
 };
 constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 // Split planes of the first P levels, per scene: the scales n / (hi - lo) of
-// x, y and z and a pad float, then per axis the n + 1 planes P_0 = lo, ...,
-// P_n = hi of the n = 2^P depth-P cells and a pad float, the scene's block
-// rounded up to 16 bytes. A launch stages the deepest P (at most 6, at most
+// x, y and z and a pad float, the offsets -lo * scale - 0.25 of x, y and z and
+// a pad float, then per axis the n + 1 planes P_0 = lo, ..., P_n = hi of the
+// n = 2^P depth-P cells and a pad float, the scene's block rounded up to 16
+// bytes. A launch stages the deepest P (at most 6, at most
 // two levels above the cell table) whose scene table and planes fit kPlaneLds
 // bytes (seven 256-thread workgroups, 7 waves per SIMD, within a CU's 160 KiB
 // of LDS); failing that, the deepest that fits kPlaneLdsWide (five
@@ -168,14 +169,18 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 constexpr size_t kPlaneLds = 22528;
 constexpr size_t kPlaneLdsWide = 32512;
 __host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
-__host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) { return (4u + 3u * axis_stride(depth) + 3u) & ~3u; }
+constexpr uint32_t kPlaneHeader = 8;  // floats before the planes: scales, pad, offsets, pad
+__host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) {
+    return (kPlaneHeader + 3u * axis_stride(depth) + 3u) & ~3u;
+}
 
-// Split planes of one axis for n = 2^D cells (pl[k] = P_k, then the pad) and
-// its scale, nested midpoints computed with the descent's own operations
-// (kernel.cu:165-176), so cell boxes are the descent's boxes bit for bit.
-// Returns whether they support the direct cell lookup of plane_cell: finite,
-// each within 0.2 cell of the uniform grid, and an accurate scale.
-__device__ bool make_planes(float lo, float hi, uint32_t n, float* pl, float& scale_out) {
+// Split planes of one axis for n = 2^D cells (pl[k] = P_k, then the pad), its
+// scale and offset, nested midpoints computed with the descent's own
+// operations (kernel.cu:165-176), so cell boxes are the descent's boxes bit
+// for bit. Returns whether they support the direct cell lookup of plane_cell:
+// finite, each within 0.2 cell of the uniform grid, an accurate scale, and an
+// offset below 2^14 in magnitude (so it is exact to 2^-10 cell).
+__device__ bool make_planes(float lo, float hi, uint32_t n, float* pl, float& scale_out, float& off_out) {
     pl[0] = lo;
     pl[n] = hi;
     // once per workgroup: kept rolled (unrolled, it would crowd the registers
@@ -186,26 +191,30 @@ __device__ bool make_planes(float lo, float hi, uint32_t n, float* pl, float& sc
         for (uint32_t k = 0; k < n; k += step) pl[k + step / 2] = (pl[k] + pl[k + step]) * 0.5f;
     const float w = hi - lo;
     const float scale = static_cast<float>(n) / w;
+    const float off = __builtin_fmaf(-lo, scale, -0.25f);
     const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / n;
     bool ok = w > 0.0f && w <= 0x1p127f && scale > 0.0f && scale <= 0x1p127f && cw > 0.0 &&
-              fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6;
+              fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6 && fabsf(off) <= 0x1p14f;
 #pragma unroll 1
     for (uint32_t k = 0; k <= n; ++k)
         ok = ok && fabs(static_cast<double>(pl[k]) - (static_cast<double>(lo) + k * cw)) <= 0.2 * cw;
     scale_out = scale;
+    off_out = off;
     pl[n + 1] = 0.0f;
     return ok;
 }
 
-// Depth-D cell of p along one axis from its planes (pl[k] = P_k, P_0 = lo)
-// and scale, and the cell's bounds. With planes within 0.2 cell of uniform,
-// u = (p - P_0) * scale - 0.25 lies within (j - 0.46, j + 0.96) for the cell j
-// that holds p (P_j <= p < P_j+1, or j = n - 1 at p = P_n), so trunc(u) is
-// j - 1 or j (0 when u < 0, where j is 0); capped at n - 2 it is still j - 1
-// or j, and one comparison with the next plane settles it.
-__device__ __forceinline__ uint32_t plane_cell(float p, float lo0, float scale, const float* pl, uint32_t n, float& lo,
+// Depth-D cell of p along one axis from its planes (pl[k] = P_k, P_0 = lo),
+// scale and offset, and the cell's bounds. With planes within 0.2 cell of
+// uniform, an offset exact to 2^-10 cell and an accurate scale,
+// u = p * scale + offset ~ (p - P_0) * scale - 0.25 lies within
+// (j - 0.47, j + 0.97) for the cell j that holds p (P_j <= p < P_j+1, or
+// j = n - 1 at p = P_n), so trunc(u) is j - 1 or j (0 when u < 0, where j is
+// 0); capped at n - 2 it is still j - 1 or j, and one comparison with the
+// next plane settles it.
+__device__ __forceinline__ uint32_t plane_cell(float p, float off, float scale, const float* pl, uint32_t n, float& lo,
                                                float& hi) {
-    const float u = __builtin_fmaf(p - lo0, scale, -0.25f);
+    const float u = __builtin_fmaf(p, scale, off);
     const uint32_t j0 = min(static_cast<uint32_t>(static_cast<int32_t>(u)), n - 2u);
     const float a = pl[j0], b = pl[j0 + 1], c = pl[j0 + 2];
     const bool up = p >= b;
@@ -218,49 +227,24 @@ __device__ __forceinline__ uint32_t plane_cell(float p, float lo0, float scale, 
 // kDepth the cell-table depth (kPD <= kDepth <= kPD + 2: a depth-kDepth cell is
 // kDepth - kPD splits below its depth-kPD cell); kPD = 0: no planes, the table
 // depth is P.cell_depth and cells come from splits.
-template <int kDepth, int kPD, bool kPoses>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
+// The march of one launch (everything after the workgroup's set-up). kFast:
+// the launch has split planes and tame, shallow, monotone scenes (no void
+// cache, no depth counter, no range checks); the flags are then compile-time
+// constants, and everything the other launches need is compiled out.
+template <int kDepth, int kPD, bool kPoses, bool kFast>
+__device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scenes, float* lds_planes, int tame,
+                                      int shallow, int planes, bool void_cache) {
     constexpr bool kPlanes = kPD > 0;
-    static_assert(!kPlanes || (kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7),
-                  "planes of 4..6 levels, the table at most two levels below them");
-    extern __shared__ SceneLds lds_scenes[];
-    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
-    // `tame`: every scene box has coordinates below 2^100 in magnitude, so
-    // lo + hi never overflows, every split plane lies within its box, each
-    // descent box lies within its parent and the domain, and exit quotients
-    // (numerators below 2^101, divisors above 1e-4) stay far from overflow.
-    // `shallow`: no record of any scene lies deeper than 30 levels, so every
-    // slot a descent reads is at depth <= 31 and the 32-level limit of
-    // kernel.cu:136 never applies.
-    int tame = 1, shallow = 1;
-    for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
-        const navi_relaid_scene d = P.scenes[i];
-        lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
-                                 d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
-        for (int a = 0; a < 3; ++a)
-            tame &= (fabsf(d.bbox_min[a]) < 0x1p100f && fabsf(d.bbox_max[a]) < 0x1p100f) ? 1 : 0;
-        shallow &= d.max_depth <= static_cast<uint32_t>(kMaxDepth - 2) ? 1 : 0;
+    if (kFast) {
+        tame = 1;
+        shallow = 1;
+        planes = 1;
+        void_cache = false;
     }
-    tame = __syncthreads_and(tame);
-    shallow = __syncthreads_and(shallow);
-    // `planes`: every scene's depth-D cells can be located from its planes
-    int planes = kPlanes ? 1 : 0;
     const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
     constexpr uint32_t kAxis = kPlanes ? axis_stride(kPD) : 0u;    // floats per axis
     constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
     constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
-    if (kPlanes) {
-        for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
-            const navi_relaid_scene& d = P.scenes[i / 3];
-            const int a = i % 3;
-            float* hdr = lds_planes + (i / 3) * kScene;
-            float scale = 0.0f;
-            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], kCells, hdr + 4 + a * kAxis, scale) ? 1 : 0;
-            hdr[a] = scale;
-            if (a == 0) hdr[3] = 0.0f;
-        }
-        planes = __syncthreads_and(planes);
-    }
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     // The record pool as a buffer resource: 32-bit byte offsets, and the
@@ -285,11 +269,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     int32_t sem = 0, step = 0;
     uint32_t scene = 0;  // this ray's scene (an index into lds_scenes)
     Box lf{}, vd{};
-    // The prefix cache (kernel.cu:120-132, 154-163) as the cell's depth-4
-    // indices x | y << 4 | z << 8. The plane kernels keep no box for it: the
-    // plane lookup of p decides containment in integers. Without planes the
-    // box is kept (kDepth = 0) or rebuilt by four splits (planes switched off
-    // for the launch).
+    // The prefix cache (kernel.cu:120-132, 154-163). The plane kernels keep
+    // the cached depth-4 cell as the depth-kPD plane index of its upper face
+    // per axis, x | y << 8 | z << 16, all ones when nothing is cached, and no
+    // box: the plane lookup of p decides in integers. Otherwise the cell's
+    // depth-4 indices x | y << 4 | z << 8 (valid with pre_ok), with its box
+    // kept (kDepth = 0) or rebuilt by four splits (planes switched off for
+    // the launch).
     Box pre{};
     uint32_t lf_slot = 0;
     uint32_t pre_cell = 0;
@@ -369,6 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                 sem = 0;
                 step = 0;
                 lf_ok = vd_ok = pre_ok = false;
+                pre_cell = 0xffffffffu;
                 has_ray = true;
                 if (sc < 0 || sc >= P.n_scenes) {
                     // unknown scene: report like a fault, no steps
@@ -409,7 +396,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // the cache tests in the reference's order, as exclusive outcomes:
         // void cache (kernel.cu:265-267), outside the domain (:108-112), leaf
         // cache (:114-118); one-leaf scenes always end here
-        const bool hit_vd = vd_ok && in_box_strict(px, py, pz, vd);
+        const bool hit_vd = void_cache && vd_ok && in_box_strict(px, py, pz, vd);
         const bool outside = !hit_vd && !in_box(px, py, pz, dom);
         const bool hit_lf = !hit_vd && !outside && lf_ok && in_box(px, py, pz, lf);
         bool descending = has_ray && !(hit_vd || outside || hit_lf);
@@ -431,28 +418,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         if (descending) {
             // the scene's scales and planes of x, y, z
             const float* hdr = lds_planes + __umul24(scene, kScene);
-            const float* plx = hdr + 4;
+            const float* plx = hdr + kPlaneHeader;
             const float* ply = plx + kAxis;
             const float* plz = ply + kAxis;
             uint32_t jx = 0, jy = 0, jz = 0;
             bool use_pre;
             if (kPlanes && planes) {
                 const float4 scale = *reinterpret_cast<const float4*>(hdr);
-                jx = plane_cell(px, dom.x0, scale.x, plx, kCells, cur.x0, cur.x1);
-                jy = plane_cell(py, dom.y0, scale.y, ply, kCells, cur.y0, cur.y1);
-                jz = plane_cell(pz, dom.z0, scale.z, plz, kCells, cur.z0, cur.z1);
+                const float4 offs = *reinterpret_cast<const float4*>(hdr + 4);
+                jx = plane_cell(px, offs.x, scale.x, plx, kCells, cur.x0, cur.x1);
+                jy = plane_cell(py, offs.y, scale.y, ply, kCells, cur.y0, cur.y1);
+                jz = plane_cell(pz, offs.z, scale.z, plz, kCells, cur.z0, cur.z1);
                 // The prefix cell holds p, faces included (kernel.cu:120-132),
                 // when per axis p's cell lies in it or p is on its upper face,
-                // where p's cell starts (p == its lower plane). The domain's
-                // upper face is inside: there p's cell is the last one.
+                // where p's cell starts (p == its lower plane; the domain's
+                // upper face is inside: there p's cell is the last one). A
+                // descent from it meets the cell a fresh descent meets (the
+                // saved prefix is then the one already cached), except when p
+                // is on an upper face: only then does the prefix matter.
                 constexpr uint32_t sh = kPD - kPrefixDepth;
-                const uint32_t kx = pre_cell & 15u, ky = (pre_cell >> 4) & 15u, kz = pre_cell >> 8;
-                const bool fx = jx == ((kx + 1u) << sh) && px == cur.x0;
-                const bool fy = jy == ((ky + 1u) << sh) && py == cur.y0;
-                const bool fz = jz == ((kz + 1u) << sh) && pz == cur.z0;
-                use_pre = pre_ok && ((jx >> sh) == kx || fx) && ((jy >> sh) == ky || fy) && ((jz >> sh) == kz || fz);
+                const uint32_t ux = pre_cell & 0xffu, uy = (pre_cell >> 8) & 0xffu, uz = pre_cell >> 16;
+                const bool fx = jx == ux && px == cur.x0;
+                const bool fy = jy == uy && py == cur.y0;
+                const bool fz = jz == uz && pz == cur.z0;
+                use_pre = (fx || fy || fz) && (fx || (jx >> sh) + 1u == (ux >> sh)) &&
+                          (fy || (jy >> sh) + 1u == (uy >> sh)) && (fz || (jz >> sh) + 1u == (uz >> sh));
                 // on an upper face the descent from the prefix cell stays in it
-                if (use_pre && (fx || fy || fz)) {  // rare
+                if (use_pre) {  // rare
                     jx -= fx ? 1u : 0u;
                     jy -= fy ? 1u : 0u;
                     jz -= fz ? 1u : 0u;
@@ -568,7 +560,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             }
             // kernel.cu:154-163: a fresh descent caches the depth-4 node when it
             // is internal, i.e. when the path goes below depth 4; the cell is
-            // the depth-4 ancestor of the depth-D cell
+            // the depth-4 ancestor of the depth-D cell. (The plane kernels
+            // re-save the cached cell on the prefix descents that meet the
+            // fresh descent's cell: the same value.)
             const bool save = !use_pre && (depth > kPrefixDepth || (depth == kPrefixDepth && slot < kSlotBadChild));
             if (save) {
                 const uint32_t sh = D - kPrefixDepth;
@@ -580,7 +574,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
                         split_box(pre, ((kx >> b) & 1u) | (((ky >> b) & 1u) << 1) | (((kz >> b) & 1u) << 2));
                     }
                 }
-                pre_cell = kx | (ky << 4) | (kz << 8);
+                if (kPlanes && planes) {
+                    constexpr uint32_t up = kPlanes ? kPD - kPrefixDepth : 0u;
+                    pre_cell = ((kx + 1u) << up) | (((ky + 1u) << up) << 8) | (((kz + 1u) << up) << 16);
+                } else {
+                    pre_cell = kx | (ky << 4) | (kz << 8);
+                }
                 pre_ok = true;
             }
             cur_rec = slot;
@@ -629,13 +628,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         const bool is_void = hit_vd || new_void;
         const bool is_leaf = hit_lf || new_leaf;
         const bool is_fault = slot == kSlotFault;
-        vd.x0 = new_void ? cur.x0 : vd.x0;
-        vd.y0 = new_void ? cur.y0 : vd.y0;
-        vd.z0 = new_void ? cur.z0 : vd.z0;
-        vd.x1 = new_void ? cur.x1 : vd.x1;
-        vd.y1 = new_void ? cur.y1 : vd.y1;
-        vd.z1 = new_void ? cur.z1 : vd.z1;
-        vd_ok = vd_ok || new_void;
+        if (void_cache) {
+            vd.x0 = new_void ? cur.x0 : vd.x0;
+            vd.y0 = new_void ? cur.y0 : vd.y0;
+            vd.z0 = new_void ? cur.z0 : vd.z0;
+            vd.x1 = new_void ? cur.x1 : vd.x1;
+            vd.y1 = new_void ? cur.y1 : vd.y1;
+            vd.z1 = new_void ? cur.z1 : vd.z1;
+            vd_ok = vd_ok || new_void;
+        }
         lf.x0 = new_leaf ? cur.x0 : lf.x0;
         lf.y0 = new_leaf ? cur.y0 : lf.y0;
         lf.z0 = new_leaf ? cur.z0 : lf.z0;
@@ -649,9 +650,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         // kernel.cu:54-85 on the void box, branch-free: the face per axis is
         // fixed by the direction's sign; axes with |d| <= 1e-4 have a NaN
         // reciprocal and drop out of the minimum.
-        const float nx = (dx > 0.f ? vd.x1 : vd.x0) - px;
-        const float ny = (dy > 0.f ? vd.y1 : vd.y0) - py;
-        const float nz = (dz > 0.f ? vd.z1 : vd.z0) - pz;
+        // (without the void cache every void step found its cell just now)
+        float nx, ny, nz;
+        if (void_cache) {
+            nx = (dx > 0.f ? vd.x1 : vd.x0) - px;
+            ny = (dy > 0.f ? vd.y1 : vd.y0) - py;
+            nz = (dz > 0.f ? vd.z1 : vd.z0) - pz;
+        } else {
+            nx = (dx > 0.f ? cur.x1 : cur.x0) - px;
+            ny = (dy > 0.f ? cur.y1 : cur.y0) - py;
+            nz = (dz > 0.f ? cur.z1 : cur.z0) - pz;
+        }
         float e;
         if (tame) {
             e = fminf(fminf(fminf(markstein(nx, dx, rx), markstein(ny, dy, ry)), markstein(nz, dz, rz)),
@@ -718,6 +727,72 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
             if (P.out_steps) P.out_steps[ray] = step;
         }
     }
+}
+
+template <int kDepth, int kPD, bool kPoses>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
+    constexpr bool kPlanes = kPD > 0;
+    static_assert(!kPlanes || (kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7),
+                  "planes of 4..6 levels, the table at most two levels below them");
+    extern __shared__ SceneLds lds_scenes[];
+    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
+    // `tame`: every scene box has coordinates below 2^100 in magnitude, so
+    // lo + hi never overflows, every split plane lies within its box, each
+    // descent box lies within its parent and the domain, and exit quotients
+    // (numerators below 2^101, divisors above 1e-4) stay far from overflow.
+    // `shallow`: no record of any scene lies deeper than 30 levels, so every
+    // slot a descent reads is at depth <= 31 and the 32-level limit of
+    // kernel.cu:136 never applies. `monotone`: no scene has a negative leaf
+    // distance, so t never decreases along a ray.
+    int tame = 1, shallow = 1, monotone = 1;
+    for (int32_t i = threadIdx.x; i < P.n_scenes; i += blockDim.x) {
+        const navi_relaid_scene d = P.scenes[i];
+        lds_scenes[i] = SceneLds{d.bbox_min[0], d.bbox_min[1], d.bbox_min[2],
+                                 d.bbox_max[0], d.bbox_max[1], d.bbox_max[2], d.root_slot, 0u};
+        for (int a = 0; a < 3; ++a)
+            tame &= (fabsf(d.bbox_min[a]) < 0x1p100f && fabsf(d.bbox_max[a]) < 0x1p100f) ? 1 : 0;
+        shallow &= d.max_depth <= static_cast<uint32_t>(kMaxDepth - 2) ? 1 : 0;
+        monotone &= (d.flags & NAVI_SCENE_NONNEG_LEAVES) ? 1 : 0;
+    }
+    tame = __syncthreads_and(tame);
+    shallow = __syncthreads_and(shallow);
+    // The void cache (kernel.cu:265-267) changes nothing in tame, monotone
+    // launches: a point strictly inside the cached void cell lies in the
+    // closed box of no other terminal cell (tame boxes nest), so the leaf
+    // cache misses and a query meets that cell again, with the same exit
+    // distance. Along a ray whose t never decreases the samples inside the
+    // open cell are consecutive, right after the step that found it, so the
+    // prefix cache then holds that cell's depth-4 ancestor (when it is deeper
+    // than 4; else the query stops above depth 4 and saves nothing) and the
+    // query leaves every cache as it was. Such launches skip the void cache.
+    const bool void_cache = !(tame && __syncthreads_and(monotone));
+    // `planes`: every scene's depth-D cells can be located from its planes
+    int planes = kPlanes ? 1 : 0;
+    const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
+    constexpr uint32_t kAxis = kPlanes ? axis_stride(kPD) : 0u;    // floats per axis
+    constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
+    constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
+    if (kPlanes) {
+        for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
+            const navi_relaid_scene& d = P.scenes[i / 3];
+            const int a = i % 3;
+            float* hdr = lds_planes + (i / 3) * kScene;
+            float scale = 0.0f, off = 0.0f;
+            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], kCells, hdr + kPlaneHeader + a * kAxis, scale, off)
+                          ? 1 : 0;
+            hdr[a] = scale;
+            hdr[4 + a] = off;
+            if (a == 0) hdr[3] = hdr[7] = 0.0f;
+        }
+        planes = __syncthreads_and(planes);
+    }
+    const bool fast = kPlanes && planes && tame && shallow && !void_cache;
+    if (fast)
+        march<kDepth, kPD, kPoses, true>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
+    else
+        march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
     // The last wave to finish rearms the queue for the next launch on this
     // stream: every other wave has made its final claim before counting itself.
     if (P.queue != nullptr && lane == 0) {

@@ -39,7 +39,8 @@ PLANE_LDS_BYTES_WIDE = 32512
 
 
 def _plane_bytes(depth: int) -> int:
-    return 4 * ((4 + 3 * ((1 << depth) + 2) + 3) & ~3)
+    # scene_stride in trace_relaid.hip: 8 header floats, then 2^depth + 2 per axis
+    return 4 * ((8 + 3 * ((1 << depth) + 2) + 3) & ~3)
 
 
 def plane_depth(n_scenes: int, table_depth: int) -> int:
@@ -139,6 +140,8 @@ class ResidentScenes:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
             for i in range(len(scenes)):
                 rtable[i]["max_depth"] = _native.record_depth(allrec[:roff], int(rtable[i]["root_slot"]))
+                if _native.nonneg_leaves(recs[i], rtable[i]["root_slot"]):
+                    rtable[i]["flags"] |= _native.SCENE_NONNEG_LEAVES
             if table_depth is not None:
                 self.table_depth = int(table_depth)
             else:
