@@ -113,6 +113,7 @@ struct RelaidParams {
     uint32_t* __restrict__ queue;  // [next unit, finished waves], or null: static schedule
     uint32_t n_units;              // work units of unit_rays rays
     uint32_t unit_rays;            // 128 (2 tiles), or 64 for batches too small to fill the chip
+    uint32_t small_tables;         // the cell tables span fewer than 2^32 bytes
 };
 
 // Work index q -> ray id (env * R + r).
@@ -227,6 +228,361 @@ __device__ __forceinline__ uint32_t plane_cell(float p, float off, float scale, 
 // kDepth the cell-table depth (kPD <= kDepth <= kPD + 2: a depth-kDepth cell is
 // kDepth - kPD splits below its depth-kPD cell); kPD = 0: no planes, the table
 // depth is P.cell_depth and cells come from splits.
+// Wave-uniform work distribution of one wave: a static sequence of 64-ray
+// chunks (wave, wave + n_waves, ...) without a queue, else work units claimed
+// from the queue, `unit_used` rays of `unit` handed out so far.
+struct Sched {
+    uint32_t wave, n_waves, seq_end, seq_next, unit, unit_used;
+    bool exhausted;
+};
+
+__device__ __forceinline__ Sched sched_init(const RelaidParams& P) {
+    Sched S;
+    S.wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
+    S.n_waves = (gridDim.x * blockDim.x) >> 6;
+    const uint32_t my_chunks = S.wave < P.n_chunks ? (P.n_chunks - S.wave + S.n_waves - 1) / S.n_waves : 0u;
+    S.seq_end = my_chunks * 64u;
+    S.seq_next = 0;
+    S.unit = 0;
+    S.unit_used = P.unit_rays;
+    S.exhausted = (P.queue == nullptr) ? (S.seq_end == 0) : false;
+    return S;
+}
+
+// Work indices for the wave's idle lanes (`need`, n_need of them; `rank` =
+// idle lanes below this one): this lane's index, or 0xffffffff for none.
+__device__ __forceinline__ uint32_t claim(const RelaidParams& P, Sched& S, uint32_t n_need, uint32_t rank,
+                                          uint32_t lane) {
+    uint32_t q = 0xffffffffu;
+    if (P.queue == nullptr) {
+        const uint32_t sq = S.seq_next + rank;
+        if (sq < S.seq_end) q = (S.wave + (sq >> 6) * S.n_waves) * 64u + (sq & 63u);
+        S.seq_next += n_need;
+        S.exhausted = S.seq_next >= S.seq_end;
+    } else {
+        const uint32_t avail = P.unit_rays - S.unit_used;
+        if (rank < avail) q = S.unit * P.unit_rays + S.unit_used + rank;
+        if (n_need > avail) {
+            uint32_t claimed = 0;
+            if (lane == 0) claimed = atomicAdd(P.queue, 1u);
+            claimed = __builtin_amdgcn_readlane(claimed, 0);
+            if (claimed < P.n_units) {
+                if (rank >= avail) q = claimed * P.unit_rays + (rank - avail);
+                S.unit = claimed;
+                S.unit_used = n_need - avail;
+            } else {
+                S.exhausted = true;
+                S.unit_used = P.unit_rays;
+            }
+        } else {
+            S.unit_used += n_need;
+        }
+    }
+    return q;
+}
+
+struct Float3 {
+    float x, y, z;
+};
+
+// A ray as its march starts: id, scene, origin, direction and the exit
+// reciprocals.
+struct RayStart {
+    uint32_t ray, scene;
+    float ox, oy, oz, dx, dy, dz, rx, ry, rz;
+};
+
+// Loads the ray of work index q. Returns 1 for a ray to march, 0 for none
+// (q beyond the batch, or an env_order entry outside [0, n_envs): skipped),
+// and 2 for a ray of an unknown scene, already reported like a fault.
+template <bool kPoses>
+__device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayStart& R) {
+    if (q >= P.n_rays) return 0;
+    int32_t env = 0;
+    R.ray = ray_of(P, q, env);
+    if (static_cast<uint32_t>(env) >= P.n_envs) return 0;
+    const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
+    if (kPoses) {
+        // sdfdag_backend.py:1300-1312: origin = the env's position;
+        // x' = x c + z s, y' = y, z' = (-x) s + z c, each product
+        // and sum rounded on its own as in the eager tensor code
+        const uint32_t r = R.ray - static_cast<uint32_t>(env) * P.rays_per_env;
+        const float c = P.env_rot[2 * env], s = P.env_rot[2 * env + 1];
+        const float lx = P.local_dirs[3 * r + 0];
+        const float ly = P.local_dirs[3 * r + 1];
+        const float lz = P.local_dirs[3 * r + 2];
+        R.ox = P.env_pos[3 * env + 0];
+        R.oy = P.env_pos[3 * env + 1];
+        R.oz = P.env_pos[3 * env + 2];
+        R.dx = lx * c + lz * s;
+        R.dy = ly;
+        R.dz = (-lx) * s + lz * c;
+    } else {
+        // one 12-byte load per vector (a wave's lanes then touch each cache
+        // line of the AoS arrays once, not three times)
+        const Float3 o = *reinterpret_cast<const Float3*>(P.origins + 3 * R.ray);
+        const Float3 d = *reinterpret_cast<const Float3*>(P.dirs + 3 * R.ray);
+        R.ox = o.x;
+        R.oy = o.y;
+        R.oz = o.z;
+        R.dx = d.x;
+        R.dy = d.y;
+        R.dz = d.z;
+    }
+    // correctly rounded reciprocals (IEEE division) of the axes the exit uses
+    // (|d| > 1e-4, kernel.cu:54-85); NaN marks the others, whose quotients
+    // fminf then ignores
+    R.rx = (R.dx > kDirEps || R.dx < -kDirEps) ? 1.0f / R.dx : __builtin_nanf("");
+    R.ry = (R.dy > kDirEps || R.dy < -kDirEps) ? 1.0f / R.dy : __builtin_nanf("");
+    R.rz = (R.dz > kDirEps || R.dz < -kDirEps) ? 1.0f / R.dz : __builtin_nanf("");
+    if (sc < 0 || sc >= P.n_scenes) {
+        // unknown scene: report like a fault, no steps
+        P.out_d[R.ray] = __builtin_nanf("");
+        P.out_s[R.ray] = 0;
+        if (P.out_steps) P.out_steps[R.ray] = 0;
+        return 2;
+    }
+    R.scene = static_cast<uint32_t>(sc);
+    return 1;
+}
+
+// The fast march: launches whose scenes all have split planes in LDS, tame
+// boxes, no record deeper than 30 levels and no negative leaf distance, with
+// cell tables below 4 GiB (every scene the library's compiler writes). Per ray
+// the results are the general march's; it leaves out what such launches
+// cannot meet: the void cache (it changes nothing in them, see the kernel), the
+// depth counter (the 32-level limit never applies) and the range checks of the
+// exit quotients and of the leaf-run step (tame boxes). Conditions are
+// combined with bitwise operators, so the step's path has no short-circuit
+// branches, and the cell table is read through a buffer resource (32-bit
+// offsets).
+template <int kDepth, int kPD, bool kPoses>
+__device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
+                                           const float* lds_planes) {
+    static_assert(kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2, "planes of 4..6 levels");
+    constexpr uint32_t D = kDepth;                    // the table depth
+    constexpr uint32_t kAxis = axis_stride(kPD);      // floats per axis
+    constexpr uint32_t kScene = scene_stride(kPD);    // floats per scene
+    constexpr uint32_t kCells = 1u << kPD;            // cells per axis
+    constexpr uint32_t kShP = kPD - kPrefixDepth;     // depth-kPD index >> kShP = depth-4 index
+    constexpr uint32_t kShD = D - kPrefixDepth;       // depth-D index >> kShD = depth-4 index
+    const uint32_t lane = threadIdx.x & 63u;
+    const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(P.records), static_cast<short>(0), static_cast<int>(P.n_records * 32u), 0x00020000);
+    const __amdgpu_buffer_rsrc_t tables = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint64_t*>(P.cell_table), static_cast<short>(0),
+        static_cast<int>(static_cast<uint32_t>(P.n_scenes) << (3u * D + 3u)), 0x00020000);
+    Sched sched = sched_init(P);
+
+    // per-lane ray state; the prefix cache as in the general march's plane
+    // kernels (depth-kPD plane index of the cached cell's upper face per axis,
+    // x | y << 8 | z << 16, all ones when nothing is cached)
+    bool has_ray = false, lf_ok = false;
+    uint32_t ray = 0, scene = 0, lf_slot = 0, pre_cell = 0xffffffffu;
+    float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
+    float t = 0.f, dist = 0.f;
+    int32_t sem = 0, step = 0;
+    Box lf{};
+
+    while (true) {
+        // ---- refill idle lanes (as the general march) ----
+        const uint64_t need = __ballot(!has_ray);
+        const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
+        if ((n_need >= kRefillMin || n_need == 64u) && !sched.exhausted) {
+            const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
+            const uint32_t q = claim(P, sched, n_need, rank, lane);
+            RayStart R;
+            if (!has_ray && start_ray<kPoses>(P, q, R) == 1) {
+                ray = R.ray;
+                scene = R.scene;
+                ox = R.ox;
+                oy = R.oy;
+                oz = R.oz;
+                dx = R.dx;
+                dy = R.dy;
+                dz = R.dz;
+                rx = R.rx;
+                ry = R.ry;
+                rz = R.rz;
+                t = 0.f;
+                dist = 0.f;
+                sem = 0;
+                step = 0;
+                pre_cell = 0xffffffffu;
+                has_ray = true;
+                // a one-leaf DAG: its leaf and the domain box (kernel.cu:139-152)
+                const SceneLds& S = lds_scenes[scene];
+                lf_ok = (S.root & 0x80000000u) != 0u;
+                lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                lf_slot = S.root;
+            }
+        }
+        if (__ballot(has_ray) == 0ull) {
+            if (sched.exhausted) break;
+            continue;
+        }
+
+        // ---- start the step: domain and leaf-cache tests (kernel.cu:108-118) ----
+        step += has_ray ? 1 : 0;
+        const SceneLds& S = lds_scenes[scene];
+        const Box dom{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+        const float px = __builtin_fmaf(t, dx, ox);
+        const float py = __builtin_fmaf(t, dy, oy);
+        const float pz = __builtin_fmaf(t, dz, oz);
+        const bool outside = !in_box(px, py, pz, dom);
+        const bool hit_lf = !outside & lf_ok & in_box(px, py, pz, lf);
+        const bool descending = has_ray & !outside & !hit_lf;
+        Box cur = dom;
+        uint32_t slot = 0;  // an internal slot: no outcome for lanes that do not descend
+
+        if (descending) {
+            // ---- the depth-kPD cell from the split planes ----
+            const float* hdr = lds_planes + __umul24(scene, kScene);
+            const float* plx = hdr + kPlaneHeader;
+            const float* ply = plx + kAxis;
+            const float* plz = ply + kAxis;
+            const float4 scale = *reinterpret_cast<const float4*>(hdr);
+            const float4 offs = *reinterpret_cast<const float4*>(hdr + 4);
+            uint32_t jx = plane_cell(px, offs.x, scale.x, plx, kCells, cur.x0, cur.x1);
+            uint32_t jy = plane_cell(py, offs.y, scale.y, ply, kCells, cur.y0, cur.y1);
+            uint32_t jz = plane_cell(pz, offs.z, scale.z, plz, kCells, cur.z0, cur.z1);
+            // the prefix cache matters only on an upper face of the cached
+            // cell (kernel.cu:120-132); see the general march
+            const uint32_t ux = pre_cell & 0xffu, uy = (pre_cell >> 8) & 0xffu, uz = pre_cell >> 16;
+            const bool fx = (jx == ux) & (px == cur.x0);
+            const bool fy = (jy == uy) & (py == cur.y0);
+            const bool fz = (jz == uz) & (pz == cur.z0);
+            bool use_pre = false;
+            if (fx | fy | fz) {  // rare
+                use_pre = (fx | ((jx >> kShP) + 1u == (ux >> kShP))) & (fy | ((jy >> kShP) + 1u == (uy >> kShP))) &
+                          (fz | ((jz >> kShP) + 1u == (uz >> kShP)));
+                if (use_pre) {
+                    jx -= fx ? 1u : 0u;
+                    jy -= fy ? 1u : 0u;
+                    jz -= fz ? 1u : 0u;
+                    const float lx = plx[jx], ly = ply[jy], lz = plz[jz];
+                    cur.x1 = fx ? cur.x0 : cur.x1;
+                    cur.y1 = fy ? cur.y0 : cur.y1;
+                    cur.z1 = fz ? cur.z0 : cur.z1;
+                    cur.x0 = fx ? lx : cur.x0;
+                    cur.y0 = fy ? ly : cur.y0;
+                    cur.z0 = fz ? lz : cur.z0;
+                }
+            }
+            // ---- splits down to the table depth (kernel.cu:165-176) ----
+#pragma unroll
+            for (uint32_t l = kPD; l < D; ++l) {
+                const float mx = (cur.x0 + cur.x1) * 0.5f;
+                const float my = (cur.y0 + cur.y1) * 0.5f;
+                const float mz = (cur.z0 + cur.z1) * 0.5f;
+                const bool gx = px >= mx, gy = py >= my, gz = pz >= mz;
+                cur.x0 = gx ? mx : cur.x0;
+                cur.x1 = gx ? cur.x1 : mx;
+                cur.y0 = gy ? my : cur.y0;
+                cur.y1 = gy ? cur.y1 : my;
+                cur.z0 = gz ? mz : cur.z0;
+                cur.z1 = gz ? cur.z1 : mz;
+                jx = append_bit(jx, gx);
+                jy = append_bit(jy, gy);
+                jz = append_bit(jz, gz);
+            }
+            // ---- one cell-table read: the slot D levels down, and its depth ----
+            const auto e = __builtin_amdgcn_raw_buffer_load_b64(
+                tables, (((((scene << D) | jz) << D | jy) << D) | jx) << 3, 0, 0);
+            slot = e[0];
+            const uint32_t depth = e[1];
+            if (depth < D) {
+                // a leaf / void / fault above depth D: its box from the planes
+                // down to depth kPD, splits below
+                const uint32_t dp = min(depth, static_cast<uint32_t>(kPD));
+                const uint32_t sh = D - dp;
+                const uint32_t up = kPD - dp;
+                const uint32_t w = 1u << up;
+                const uint32_t kx = (jx >> sh) << up, ky = (jy >> sh) << up, kz = (jz >> sh) << up;
+                cur = Box{plx[kx], ply[ky], plz[kz], plx[kx + w], ply[ky + w], plz[kz + w]};
+                if (kDepth > kPD + 1) {  // depth can lie between kPD and D
+#pragma unroll 1
+                    for (uint32_t l = static_cast<uint32_t>(kPD); l < depth; ++l) {
+                        const uint32_t b = D - 1u - l;
+                        split_box(cur, ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2));
+                    }
+                }
+            }
+            // kernel.cu:154-163: a fresh descent caches its depth-4 cell when the
+            // path goes below depth 4 (prefix descents meeting the fresh
+            // descent's cell re-save the cell they hold)
+            const bool save = !use_pre & ((depth > kPrefixDepth) |
+                                          ((depth == kPrefixDepth) & (slot < kSlotBadChild)));
+            const uint32_t saved = (((jx >> kShD) + 1u) << kShP) | ((((jy >> kShD) + 1u) << kShP) << 8) |
+                                   ((((jz >> kShD) + 1u) << kShP) << 16);
+            pre_cell = save ? saved : pre_cell;
+
+            // ---- below depth D: one 4-byte slot per level (kernel.cu:136-199) ----
+            // (at most 32 - D trips, see the general march)
+            uint32_t cur_rec = slot;
+            bool deeper = slot < kSlotBadChild;
+            for (uint32_t trip = D; deeper && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
+                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
+                cur_rec = slot;
+                deeper = slot < kSlotBadChild;
+            }
+        }
+
+        // ---- the query's outcome and the leaf cache ----
+        const bool new_leaf = (slot & 0x80000000u) != 0u;
+        const bool new_void = slot == kSlotVoid;
+        const bool is_fault = slot == kSlotFault;
+        const bool is_leaf = hit_lf | new_leaf;
+        lf.x0 = new_leaf ? cur.x0 : lf.x0;
+        lf.y0 = new_leaf ? cur.y0 : lf.y0;
+        lf.z0 = new_leaf ? cur.z0 : lf.z0;
+        lf.x1 = new_leaf ? cur.x1 : lf.x1;
+        lf.y1 = new_leaf ? cur.y1 : lf.y1;
+        lf.z1 = new_leaf ? cur.z1 : lf.z1;
+        lf_slot = new_leaf ? slot : lf_slot;
+        lf_ok = lf_ok | new_leaf;
+
+        // ---- finish the step (kernel.cu:54-85, 297-308) ----
+        const float nx = (dx > 0.f ? cur.x1 : cur.x0) - px;
+        const float ny = (dy > 0.f ? cur.y1 : cur.y0) - py;
+        const float nz = (dz > 0.f ? cur.z1 : cur.z0) - pz;
+        const float e = fminf(fminf(fminf(markstein(nx, dx, rx), markstein(ny, dy, ry)), markstein(nz, dz, rz)),
+                              kOutsideDomain);
+        const float void_d = e > kVoidAdvanceEps ? e : kVoidAdvanceEps;  // fmaxf: e is never NaN
+        const float leaf_d = half_to_float(lf_slot & 0xffffu);
+        const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
+        dist = new_void ? void_d : (is_leaf ? leaf_d : (outside ? kOutsideDomain : dist));
+        sem = new_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
+        const bool hit = !is_fault & (sem != 0) & (dist < P.hit_eps);
+        const float t_next = t + dist;
+        bool finish = has_ray & (is_fault | hit | (t_next > P.max_distance) | (step >= P.max_steps));
+        t = (has_ray & !hit) ? t_next : t;
+        t = (finish & is_fault) ? __builtin_nanf("") : t;
+        sem = (finish & !hit) ? 0 : sem;
+        bool live = has_ray & !finish;
+
+        // ---- one more step if the leaf cache answers it alone ----
+        // (within the leaf box neither the void cache nor the domain test can
+        // fire for tame boxes; it repeats the leaf's distance, so it cannot hit)
+        const float qx = __builtin_fmaf(t, dx, ox);
+        const float qy = __builtin_fmaf(t, dy, oy);
+        const float qz = __builtin_fmaf(t, dz, oz);
+        const bool run = live & is_leaf & in_box(qx, qy, qz, lf);
+        step += run ? 1 : 0;
+        t = run ? t + dist : t;
+        const bool fin2 = run & ((t > P.max_distance) | (step >= P.max_steps));
+        sem = fin2 ? 0 : sem;
+        finish = finish | fin2;
+        has_ray = live & !fin2;
+        if (finish) {
+            P.out_d[ray] = t;
+            P.out_s[ray] = sem;
+            if (P.out_steps) P.out_steps[ray] = step;
+        }
+    }
+}
+
 // The march of one launch (everything after the workgroup's set-up). kFast:
 // the launch has split planes and tame, shallow, monotone scenes (no void
 // cache, no depth counter, no range checks); the flags are then compile-time
@@ -246,20 +602,12 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
     constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
     constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane((blockIdx.x * blockDim.x + threadIdx.x) >> 6);
     // The record pool as a buffer resource: 32-bit byte offsets, and the
     // hardware bounds every read by the pool's size (at most 2^27 records,
     // 4 GiB). Dword 3 = 0x00020000: 32-bit data format, as gfx9 raw buffers need.
     const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(P.records), static_cast<short>(0), static_cast<int>(P.n_records * 32u), 0x00020000);
-    const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
-    // Static schedule: this wave's chunks are wave, wave + n_waves, ...
-    const uint32_t my_chunks = wave < P.n_chunks ? (P.n_chunks - wave + n_waves - 1) / n_waves : 0u;
-    const uint32_t seq_end = my_chunks * 64u;
-    uint32_t seq_next = 0;  // wave-uniform
-    // Dynamic schedule: units claimed from the queue, `unit_used` rays of `unit` handed out.
-    uint32_t unit = 0, unit_used = P.unit_rays;
-    bool exhausted = (P.queue == nullptr) ? (seq_end == 0) : false;
+    Sched sched = sched_init(P);
 
     // per-lane ray state
     bool has_ray = false;
@@ -287,69 +635,24 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
         // block costs the whole wave, idle lanes only their own slot.
         const uint64_t need = __ballot(!has_ray);
         const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
-        if ((n_need >= kRefillMin || n_need == 64u) && !exhausted) {
+        if ((n_need >= kRefillMin || n_need == 64u) && !sched.exhausted) {
             // idle lanes below this one (mbcnt: set bits of `need` under the lane)
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
-            uint32_t q = 0xffffffffu;
-            if (P.queue == nullptr) {
-                const uint32_t sq = seq_next + rank;
-                if (sq < seq_end) q = (wave + (sq >> 6) * n_waves) * 64u + (sq & 63u);
-                seq_next += n_need;
-                exhausted = seq_next >= seq_end;
-            } else {
-                const uint32_t avail = P.unit_rays - unit_used;
-                if (rank < avail) q = unit * P.unit_rays + unit_used + rank;
-                if (n_need > avail) {
-                    uint32_t claimed = 0;
-                    if (lane == 0) claimed = atomicAdd(P.queue, 1u);
-                    claimed = __builtin_amdgcn_readlane(claimed, 0);
-                    if (claimed < P.n_units) {
-                        if (rank >= avail) q = claimed * P.unit_rays + (rank - avail);
-                        unit = claimed;
-                        unit_used = n_need - avail;
-                    } else {
-                        exhausted = true;
-                        unit_used = P.unit_rays;
-                    }
-                } else {
-                    unit_used += n_need;
-                }
-            }
-            int32_t env = 0;
-            if (!has_ray && q < P.n_rays) ray = ray_of(P, q, env);
-            // env_order entries outside [0, n_envs) name no rays: skipped
-            if (!has_ray && q < P.n_rays && static_cast<uint32_t>(env) < P.n_envs) {
-                const int32_t sc = P.env_scene ? P.env_scene[env] : 0;
-                if (kPoses) {
-                    // sdfdag_backend.py:1300-1312: origin = the env's position;
-                    // x' = x c + z s, y' = y, z' = (-x) s + z c, each product
-                    // and sum rounded on its own as in the eager tensor code
-                    const uint32_t r = ray - static_cast<uint32_t>(env) * P.rays_per_env;
-                    const float c = P.env_rot[2 * env], s = P.env_rot[2 * env + 1];
-                    const float lx = P.local_dirs[3 * r + 0];
-                    const float ly = P.local_dirs[3 * r + 1];
-                    const float lz = P.local_dirs[3 * r + 2];
-                    ox = P.env_pos[3 * env + 0];
-                    oy = P.env_pos[3 * env + 1];
-                    oz = P.env_pos[3 * env + 2];
-                    dx = lx * c + lz * s;
-                    dy = ly;
-                    dz = (-lx) * s + lz * c;
-                } else {
-                    ox = P.origins[3 * ray + 0];
-                    oy = P.origins[3 * ray + 1];
-                    oz = P.origins[3 * ray + 2];
-                    dx = P.dirs[3 * ray + 0];
-                    dy = P.dirs[3 * ray + 1];
-                    dz = P.dirs[3 * ray + 2];
-                }
-                // correctly rounded reciprocals (IEEE division) of the axes the
-                // exit uses (|d| > 1e-4, kernel.cu:54-85); NaN marks the others,
-                // whose quotients fminf then ignores
-                rx = (dx > kDirEps || dx < -kDirEps) ? 1.0f / dx : __builtin_nanf("");
-                ry = (dy > kDirEps || dy < -kDirEps) ? 1.0f / dy : __builtin_nanf("");
-                rz = (dz > kDirEps || dz < -kDirEps) ? 1.0f / dz : __builtin_nanf("");
+            const uint32_t q = claim(P, sched, n_need, rank, lane);
+            RayStart R;
+            if (!has_ray && start_ray<kPoses>(P, q, R) == 1) {
+                ray = R.ray;
+                scene = R.scene;
+                ox = R.ox;
+                oy = R.oy;
+                oz = R.oz;
+                dx = R.dx;
+                dy = R.dy;
+                dz = R.dz;
+                rx = R.rx;
+                ry = R.ry;
+                rz = R.rz;
                 t = 0.f;
                 dist = 0.f;
                 sem = 0;
@@ -357,29 +660,20 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
                 lf_ok = vd_ok = pre_ok = false;
                 pre_cell = 0xffffffffu;
                 has_ray = true;
-                if (sc < 0 || sc >= P.n_scenes) {
-                    // unknown scene: report like a fault, no steps
-                    P.out_d[ray] = __builtin_nanf("");
-                    P.out_s[ray] = 0;
-                    if (P.out_steps) P.out_steps[ray] = 0;
-                    has_ray = false;
-                } else {
-                    scene = static_cast<uint32_t>(sc);
-                    // A one-leaf DAG answers every in-domain query with that leaf
-                    // and the domain box (kernel.cu:139-152 at depth 0): prime the
-                    // leaf cache with it, which gives the same results as the
-                    // first query would.
-                    const SceneLds& S = lds_scenes[sc];
-                    if (S.root & 0x80000000u) {
-                        lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
-                        lf_slot = S.root;
-                        lf_ok = true;
-                    }
+                // A one-leaf DAG answers every in-domain query with that leaf
+                // and the domain box (kernel.cu:139-152 at depth 0): prime the
+                // leaf cache with it, which gives the same results as the
+                // first query would.
+                const SceneLds& S = lds_scenes[scene];
+                if (S.root & 0x80000000u) {
+                    lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                    lf_slot = S.root;
+                    lf_ok = true;
                 }
             }
         }
         if (__ballot(has_ray) == 0ull) {
-            if (exhausted) break;
+            if (sched.exhausted) break;
             continue;
         }
 
@@ -786,11 +1080,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         }
         planes = __syncthreads_and(planes);
     }
-    const bool fast = kPlanes && planes && tame && shallow && !void_cache;
-    if (fast)
-        march<kDepth, kPD, kPoses, true>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
-    else
+    if constexpr (kPlanes) {
+        if (planes && tame && shallow && !void_cache && P.small_tables)
+            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes);
+        else
+            march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
+    } else {
         march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
+    }
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
     // The last wave to finish rearms the queue for the next launch on this
@@ -912,6 +1209,7 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
     // table, whose LDS (with the scene table) fits kPlaneLds, else kPlaneLdsWide;
     // none if no P does.
     const uint32_t D = P.cell_depth;
+    P.small_tables = (static_cast<uint64_t>(P.n_scenes) << (3u * D + 3u)) < (1ull << 32) ? 1u : 0u;
     int pd = 0;
     for (const size_t budget : {kPlaneLds, kPlaneLdsWide}) {
         for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p) {
