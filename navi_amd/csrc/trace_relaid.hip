@@ -430,9 +430,11 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const float px = __builtin_fmaf(t, dx, ox);
         const float py = __builtin_fmaf(t, dy, oy);
         const float pz = __builtin_fmaf(t, dz, oz);
-        const bool outside = !in_box(px, py, pz, dom);
-        const bool hit_lf = !outside & lf_ok & in_box(px, py, pz, lf);
-        const bool descending = has_ray & !outside & !hit_lf;
+        const bool in_dom = in_box(px, py, pz, dom);
+        const bool in_lf = in_box(px, py, pz, lf);
+        const bool outside = !in_dom;
+        const bool hit_lf = in_dom && lf_ok && in_lf;
+        const bool descending = has_ray && in_dom && !hit_lf;
         Box cur = dom;
         uint32_t slot = 0;  // an internal slot: no outcome for lanes that do not descend
 
@@ -450,13 +452,15 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             // the prefix cache matters only on an upper face of the cached
             // cell (kernel.cu:120-132); see the general march
             const uint32_t ux = pre_cell & 0xffu, uy = (pre_cell >> 8) & 0xffu, uz = pre_cell >> 16;
-            const bool fx = (jx == ux) & (px == cur.x0);
-            const bool fy = (jy == uy) & (py == cur.y0);
-            const bool fz = (jz == uz) & (pz == cur.z0);
+            const bool ex = jx == ux, ey = jy == uy, ez = jz == uz;
+            const bool lx0 = px == cur.x0, ly0 = py == cur.y0, lz0 = pz == cur.z0;
+            const bool fx = ex && lx0, fy = ey && ly0, fz = ez && lz0;
             bool use_pre = false;
-            if (fx | fy | fz) {  // rare
-                use_pre = (fx | ((jx >> kShP) + 1u == (ux >> kShP))) & (fy | ((jy >> kShP) + 1u == (uy >> kShP))) &
-                          (fz | ((jz >> kShP) + 1u == (uz >> kShP)));
+            if (fx || fy || fz) {  // rare
+                const bool ix = (jx >> kShP) + 1u == (ux >> kShP);
+                const bool iy = (jy >> kShP) + 1u == (uy >> kShP);
+                const bool iz = (jz >> kShP) + 1u == (uz >> kShP);
+                use_pre = (fx || ix) && (fy || iy) && (fz || iz);
                 if (use_pre) {
                     jx -= fx ? 1u : 0u;
                     jy -= fy ? 1u : 0u;
@@ -512,8 +516,10 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             // kernel.cu:154-163: a fresh descent caches its depth-4 cell when the
             // path goes below depth 4 (prefix descents meeting the fresh
             // descent's cell re-save the cell they hold)
-            const bool save = !use_pre & ((depth > kPrefixDepth) |
-                                          ((depth == kPrefixDepth) & (slot < kSlotBadChild)));
+            const bool below4 = depth > kPrefixDepth;
+            const bool at4 = depth == kPrefixDepth;
+            const bool internal = slot < kSlotBadChild;
+            const bool save = !use_pre && (below4 || (at4 && internal));
             const uint32_t saved = (((jx >> kShD) + 1u) << kShP) | ((((jy >> kShD) + 1u) << kShP) << 8) |
                                    ((((jz >> kShD) + 1u) << kShP) << 16);
             pre_cell = save ? saved : pre_cell;
@@ -533,7 +539,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const bool new_leaf = (slot & 0x80000000u) != 0u;
         const bool new_void = slot == kSlotVoid;
         const bool is_fault = slot == kSlotFault;
-        const bool is_leaf = hit_lf | new_leaf;
+        const bool is_leaf = hit_lf || new_leaf;
         lf.x0 = new_leaf ? cur.x0 : lf.x0;
         lf.y0 = new_leaf ? cur.y0 : lf.y0;
         lf.z0 = new_leaf ? cur.z0 : lf.z0;
@@ -541,7 +547,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         lf.y1 = new_leaf ? cur.y1 : lf.y1;
         lf.z1 = new_leaf ? cur.z1 : lf.z1;
         lf_slot = new_leaf ? slot : lf_slot;
-        lf_ok = lf_ok | new_leaf;
+        lf_ok = lf_ok || new_leaf;
 
         // ---- finish the step (kernel.cu:54-85, 297-308) ----
         const float nx = (dx > 0.f ? cur.x1 : cur.x0) - px;
@@ -554,13 +560,15 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
         dist = new_void ? void_d : (is_leaf ? leaf_d : (outside ? kOutsideDomain : dist));
         sem = new_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
-        const bool hit = !is_fault & (sem != 0) & (dist < P.hit_eps);
+        const bool has_sem = sem != 0, near = dist < P.hit_eps;
+        const bool hit = !is_fault && has_sem && near;
         const float t_next = t + dist;
-        bool finish = has_ray & (is_fault | hit | (t_next > P.max_distance) | (step >= P.max_steps));
-        t = (has_ray & !hit) ? t_next : t;
-        t = (finish & is_fault) ? __builtin_nanf("") : t;
-        sem = (finish & !hit) ? 0 : sem;
-        bool live = has_ray & !finish;
+        const bool far = t_next > P.max_distance, spent = step >= P.max_steps;
+        bool finish = has_ray && (is_fault || hit || far || spent);
+        t = (has_ray && !hit) ? t_next : t;
+        t = (finish && is_fault) ? __builtin_nanf("") : t;
+        sem = (finish && !hit) ? 0 : sem;
+        const bool live = has_ray && !finish;
 
         // ---- one more step if the leaf cache answers it alone ----
         // (within the leaf box neither the void cache nor the domain test can
@@ -568,13 +576,15 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const float qx = __builtin_fmaf(t, dx, ox);
         const float qy = __builtin_fmaf(t, dy, oy);
         const float qz = __builtin_fmaf(t, dz, oz);
-        const bool run = live & is_leaf & in_box(qx, qy, qz, lf);
+        const bool in_lf2 = in_box(qx, qy, qz, lf);
+        const bool run = live && is_leaf && in_lf2;
         step += run ? 1 : 0;
         t = run ? t + dist : t;
-        const bool fin2 = run & ((t > P.max_distance) | (step >= P.max_steps));
+        const bool far2 = t > P.max_distance, spent2 = step >= P.max_steps;
+        const bool fin2 = run && (far2 || spent2);
         sem = fin2 ? 0 : sem;
-        finish = finish | fin2;
-        has_ray = live & !fin2;
+        finish = finish || fin2;
+        has_ray = live && !fin2;
         if (finish) {
             P.out_d[ray] = t;
             P.out_s[ray] = sem;
