@@ -143,6 +143,11 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
 
 constexpr uint32_t kRefillMin = 8;
 constexpr uint32_t kLeafRun = 1;  // leaf-cache steps taken after a leaf step
+// The fast march's: its step costs fewer operations, so a lane waits less on
+// a wave's longer runs (measured on the 16-scene 1024^3 batch: 2 leaf-cache
+// steps 1.5% faster than 1, refills at 12 idle lanes 1% faster than at 8).
+constexpr uint32_t kLeafRunFast = 2;
+constexpr uint32_t kRefillMinFast = 12;
 // rays per dynamically claimed work unit (2 tiles): larger units leave more rays
 // held by one wave when the queue runs dry, smaller ones cost more claims
 constexpr uint32_t kUnitRays = 128;
@@ -388,7 +393,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         // ---- refill idle lanes (as the general march) ----
         const uint64_t need = __ballot(!has_ray);
         const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
-        if ((n_need >= kRefillMin || n_need == 64u) && !sched.exhausted) {
+        if ((n_need >= kRefillMinFast || n_need == 64u) && !sched.exhausted) {
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
             const uint32_t q = claim(P, sched, n_need, rank, lane);
@@ -520,8 +525,12 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             const bool at4 = depth == kPrefixDepth;
             const bool internal = slot < kSlotBadChild;
             const bool save = !use_pre && (below4 || (at4 && internal));
-            const uint32_t saved = (((jx >> kShD) + 1u) << kShP) | ((((jy >> kShD) + 1u) << kShP) << 8) |
-                                   ((((jz >> kShD) + 1u) << kShP) << 16);
+            // per axis ((j >> kShD) + 1) << kShP, on the three indices packed in
+            // 8-bit fields (j < 128: no field carries into the next)
+            constexpr uint32_t kLow = (1u << kShD) - 1u;
+            constexpr uint32_t kKeep = (0xffu & ~kLow) * 0x010101u;
+            const uint32_t packed = jx | (jy << 8) | (jz << 16);
+            const uint32_t saved = ((packed & kKeep) >> (kShD - kShP)) + (1u << kShP) * 0x010101u;
             pre_cell = save ? saved : pre_cell;
 
             // ---- below depth D: one 4-byte slot per level (kernel.cu:136-199) ----
@@ -573,18 +582,23 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         // ---- one more step if the leaf cache answers it alone ----
         // (within the leaf box neither the void cache nor the domain test can
         // fire for tame boxes; it repeats the leaf's distance, so it cannot hit)
-        const float qx = __builtin_fmaf(t, dx, ox);
-        const float qy = __builtin_fmaf(t, dy, oy);
-        const float qz = __builtin_fmaf(t, dz, oz);
-        const bool in_lf2 = in_box(qx, qy, qz, lf);
-        const bool run = live && is_leaf && in_lf2;
-        step += run ? 1 : 0;
-        t = run ? t + dist : t;
-        const bool far2 = t > P.max_distance, spent2 = step >= P.max_steps;
-        const bool fin2 = run && (far2 || spent2);
-        sem = fin2 ? 0 : sem;
-        finish = finish || fin2;
-        has_ray = live && !fin2;
+        bool run = live && is_leaf;
+#pragma unroll
+        for (uint32_t k = 0; k < kLeafRunFast; ++k) {
+            const float qx = __builtin_fmaf(t, dx, ox);
+            const float qy = __builtin_fmaf(t, dy, oy);
+            const float qz = __builtin_fmaf(t, dz, oz);
+            const bool in_lf2 = in_box(qx, qy, qz, lf);
+            run = run && in_lf2;
+            step += run ? 1 : 0;
+            t = run ? t + dist : t;
+            const bool far2 = t > P.max_distance, spent2 = step >= P.max_steps;
+            const bool fin2 = run && (far2 || spent2);
+            sem = fin2 ? 0 : sem;
+            finish = finish || fin2;
+            run = run && !fin2;
+        }
+        has_ray = has_ray && !finish;
         if (finish) {
             P.out_d[ray] = t;
             P.out_s[ray] = sem;
