@@ -4,11 +4,12 @@
 // sdfdag_backend.py:366-473 and :1340 of the seismael/navi checkout) and
 // point-SDF queries over the device record layout, fused into one launch.
 //
-// Post-pass: one workgroup per env. The env's Az * El distances (flat index
-// az * El + el) are read once, coalesced; every thread keeps counts and the
-// minimum in registers, the workgroup reduces them through LDS, and thread 0
-// writes the env's statistics. The fp16 depth is written transposed,
-// (env, 1, El, Az), the layout the policy consumes.
+// Post-pass: one workgroup per env, compiled for the set of outputs asked for.
+// The env's Az * El distances (flat index az * El + el) are read once,
+// coalesced; counts are wave ballots summed on the scalar unit, the minimum a
+// per-lane register; one LDS exchange gives thread 0 the workgroup's totals for
+// the env's statistics. The fp16 depth is written transposed, (env, 1, El, Az),
+// the layout the policy consumes, through an LDS tile with an odd row pitch.
 //
 // Point queries: one lane per point, a fresh descent with no caches (the
 // query of kernel.cu:88-200 from the root): the cell table gives the first
@@ -16,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "navi_trace.h"
 #include "trace_common.hpp"
@@ -48,7 +50,8 @@ struct PostParams {
     // divides a float32 device tensor by such a scalar as a multiplication by
     // its float reciprocal: inv_log_denom = RN(1 / RN(log1p(max_distance))).
     float saturation, inv_log_denom;
-    int32_t stage16;  // stage the transposed fp16 tile in LDS (n halves fit)
+    int32_t stage16;  // stage the transposed fp16 tile in LDS (Az even, the tile fits)
+    int32_t pitch;    // the tile's row pitch in halves: El rounded up to odd
     // point queries
     const uint32_t* __restrict__ records;
     uint32_t n_records;
@@ -62,7 +65,7 @@ struct PostParams {
     float* __restrict__ point_d;
     int32_t* __restrict__ point_s;
     int32_t* __restrict__ point_kind;  // or null
-    int32_t env_blocks;                // workgroups doing the post-pass; the rest do points
+    int32_t point_blocks;              // workgroups answering point queries; the rest do envs
 };
 
 // kernel.cu:88-200 from the root at one point, no caches. Outside the domain:
@@ -143,152 +146,220 @@ __device__ T block_sum(T v, T* lds) {
     return r;
 }
 
-// minimum over the workgroup of values that are not NaN
-__device__ float block_min(float v, float* lds) {
-    for (int off = 32; off > 0; off >>= 1) v = fminf(v, __shfl_xor(v, off));
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) lds[w] = v;
-    __syncthreads();
-    float r = lds[0];
-    for (int k = 1; k < kThreads / 64; ++k) r = fminf(r, lds[k]);
-    return r;
+// the wave's lanes for which b holds
+__device__ inline uint64_t ballot(bool b) { return __builtin_amdgcn_ballot_w64(b); }
+__device__ inline uint32_t popc(uint64_t m) { return static_cast<uint32_t>(__popcll(m)); }
+
+// the lanes l of a wave with base + l < limit, for a base uniform over the wave
+__device__ inline uint64_t lanes_below(int32_t base, int32_t limit) {
+    const int32_t c = limit - base;
+    return c <= 0 ? 0ull : c >= 64 ? ~0ull : (1ull << c) - 1ull;
 }
 
-__global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
-    if (static_cast<int32_t>(blockIdx.x) >= P.env_blocks) {
-        const int32_t i = (static_cast<int32_t>(blockIdx.x) - P.env_blocks) * kThreads + threadIdx.x;
-        if (i < P.n_points) point_query(P, i);
-        return;
-    }
-    extern __shared__ _Float16 lds16[];  // the env's (El, Az) fp16 tile when staged
-    __shared__ uint32_t lds_u[kThreads / 64];
-    __shared__ float lds_f[kThreads / 64];
+constexpr int kRed = 6;  // per-wave partials: five counts and the minimum's bits
+
+// The post-pass of one env. kObs / kDelta: the float32 observation stack and the
+// delta depth are written; kF16: the fp16 depth is not written (0), written
+// straight to its transposed place (1), or staged in the LDS tile (2).
+//
+// Element k = a * El + r (azimuth bin a, elevation bin r) belongs at t = r * Az + a
+// of the transposed fp16 depth. Staged, it goes to tile[a * pitch + r]: the reads
+// of dist are coalesced along k, so a wave's lanes write consecutive halves, and
+// the copy-out reads, for consecutive t, halves pitch apart, which falls in
+// distinct banks for every lane of a wave since pitch is odd. The counts are
+// ballots: one compare per element on the vector unit, the masks of the forward
+// sector and of the env's end computed on the scalar unit from the wave's first k.
+template <bool kObs, bool kDelta, int kF16>
+__device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint32_t* red) {
     const navi_observation& O = P.O;
-    const int32_t e = blockIdx.x;
     const int32_t az = O.azimuth_bins, el = O.elevation_bins;
     const int32_t n = az * el;
     const int64_t base = static_cast<int64_t>(e) * n;
     const float* dist = O.distances + base;
+    const int32_t tid = static_cast<int32_t>(threadIdx.x);
+    const int32_t wave0 = __builtin_amdgcn_readfirstlane(tid);  // the wave's first thread
     // sdfdag_backend.py:1510-1514: the delta is zero while the previous depth
     // sums (in absolute value) below 1e-6, i.e. before the first frame
     bool first = false;
-    if (O.delta) {
+    if constexpr (kDelta) {
         float acc = 0.0f;
-        for (int32_t k = threadIdx.x; k < n; k += kThreads) acc += fabsf(O.prev_depth[base + k]);
-        first = block_sum(acc, lds_f) < 1e-6f;
+        for (int32_t k = tid; k < n; k += kThreads) acc += fabsf(O.prev_depth[base + k]);
+        first = block_sum(acc, reinterpret_cast<float*>(red)) < 1e-6f;
+        __syncthreads();  // red is reused below
     }
     // sdfdag_backend.py:390: the first and last Az/6 azimuth bins (at least
     // one), i.e. flat indices k < fwd_lo and k >= fwd_hi
     const int32_t fwd = max(1, az / 6);
     const int32_t fwd_lo = fwd * el, fwd_hi = (az - fwd) * el;
     const bool band = O.structure_band_max > O.structure_band_min;
+    const uint64_t band_lanes = band ? ~0ull : 0ull;
+    const float maxd = O.max_distance, sat = P.saturation, prox = O.proximity_threshold;
+    const float bmin = O.structure_band_min, bmax = O.structure_band_max;
+    const float inv = P.inv_log_denom;
+    const int32_t pitch = P.pitch;
     uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0, n_nan = 0;
-    float mn = INFINITY;  // of the clamped values that are not NaN
-    // Element k = a * El + r (azimuth bin a, elevation bin r) sits at t = r * Az + a
-    // in the transposed fp16 depth. Counters use & rather than && so that
-    // they stay branch-free.
-    auto element = [&](int32_t k, int32_t t, float m) {
-        const bool valid = isfinite(m);
-        const bool nan = m != m;
-        // torch.clamp(min=0, max=max_distance): both compares are false for NaN
-        float c = m < 0.0f ? 0.0f : m;
-        c = c > O.max_distance ? O.max_distance : c;
-        mn = fminf(mn, c);
-        n_nan += nan;
-        n_sat += c >= P.saturation;
-        n_prox += valid & (c <= O.proximity_threshold);
-        const bool in_band = band & valid & (c >= O.structure_band_min) & (c <= O.structure_band_max);
-        n_band += in_band;
-        // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
-        n_fwd += static_cast<uint32_t>(in_band & (k < fwd_lo)) + static_cast<uint32_t>(in_band & (k >= fwd_hi));
-        // sdfdag_backend.py:441-443; c >= 0 here, so the log1p of non-negative
-        // arguments applies (within one ulp of the exact log1p)
-        const float q = nan ? c : fminf(fmaxf(navi_log1p_nonneg(c) * P.inv_log_denom, 0.0f), 1.0f);
-        if (O.obs) {  // sdfdag_backend.py:1516-1524: stack(depth, semantic, valid), (Az, El) order
-            float* ob = O.obs + 3 * base;
-            ob[k] = q;
-            ob[n + k] = static_cast<float>(O.semantics[base + k]);
-            ob[2 * n + k] = valid ? 1.0f : 0.0f;
-        }
-        if (O.delta) {  // sdfdag_backend.py:1509-1515
-            const float pv = O.prev_depth[base + k];
-            O.delta[base + k] = first ? 0.0f : q - pv;
-            O.prev_depth[base + k] = q;
-        }
-        if (O.depth_f16) {
-            if (P.stage16) {
-                lds16[t] = static_cast<_Float16>(q);
-            } else {
-                static_cast<_Float16*>(O.depth_f16)[base + t] = static_cast<_Float16>(q);
-            }
-        }
-    };
+    float mn = INFINITY;  // of the clamped values; with a NaN input the result is NaN anyway
     // kBatch coalesced loads in flight per thread before any is used. One
     // division per batch; then k advances by kThreads = da * El + dr, i.e. r by
-    // dr and t by dr * Az + da, with a carry of one azimuth bin when r wraps.
+    // dr and a by da, with a carry of one azimuth bin when r wraps.
     constexpr int32_t kBatch = 8;
     const int32_t da = kThreads / el, dr = kThreads - da * el;
-    const int32_t dt = dr * az + da, wrap = 1 - el * az;
-    for (int32_t k0 = threadIdx.x; k0 < n; k0 += kThreads * kBatch) {
+    auto run = [&](auto tail, int32_t b0) {
+        constexpr bool kTail = decltype(tail)::value;
+        const int32_t k0 = b0 + tid;
         float m[kBatch];
 #pragma unroll
         for (int32_t j = 0; j < kBatch; ++j) {
             const int32_t k = k0 + j * kThreads;
-            m[j] = k < n ? dist[k] : 0.0f;
+            m[j] = (!kTail || k < n) ? dist[k] : 0.0f;
         }
-        const int32_t a0 = k0 / el;
-        int32_t r = k0 - a0 * el, t = r * az + a0;
+        int32_t a = k0 / el;
+        int32_t r = k0 - a * el;
 #pragma unroll
         for (int32_t j = 0; j < kBatch; ++j) {
             const int32_t k = k0 + j * kThreads;
-            if (k < n) element(k, t, m[j]);
+            const int32_t kw = b0 + wave0 + j * kThreads;  // k of the wave's lane 0
+            const uint64_t live = kTail ? lanes_below(kw, n) : ~0ull;
+            const float x = m[j];
+            // one compare per ballot, combined on the scalar unit
+            const uint64_t nan = ballot(x != x) & live;
+            const uint64_t valid = ballot(__builtin_isfinite(x)) & live;
+            // torch.clamp(min=0, max=max_distance); NaN lanes are excluded below
+            // by their mask, so what the median gives them is never used
+            const float c = __builtin_amdgcn_fmed3f(x, 0.0f, maxd);
+            if (!kTail || k < n) mn = fminf(mn, c);
+            n_nan += popc(nan);
+            n_sat += popc(ballot(c >= sat) & live & ~nan);
+            n_prox += popc(ballot(c <= prox) & valid);
+            const uint64_t in_band = ballot(c >= bmin) & ballot(c <= bmax) & valid & band_lanes;
+            n_band += popc(in_band);
+            // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
+            n_fwd += popc(in_band & lanes_below(kw, fwd_lo)) + popc(in_band & ~lanes_below(kw, fwd_hi));
+            // sdfdag_backend.py:441-443; c >= 0 here, so the log1p of non-negative
+            // arguments applies (within one ulp of the exact log1p)
+            float lq = navi_log1p_nonneg(c);
+            asm volatile("" : "+v"(lq));  // computed for every lane: no branch around it
+            const float q = x != x ? x : fminf(fmaxf(lq * inv, 0.0f), 1.0f);
+            if (!kTail || k < n) {
+                if constexpr (kObs) {  // sdfdag_backend.py:1516-1524: stack(depth, semantic, valid), (Az, El) order
+                    float* ob = O.obs + 3 * base;
+                    ob[k] = q;
+                    ob[n + k] = static_cast<float>(O.semantics[base + k]);
+                    ob[2 * n + k] = __builtin_isfinite(x) ? 1.0f : 0.0f;
+                }
+                if constexpr (kDelta) {  // sdfdag_backend.py:1509-1515
+                    const float pv = O.prev_depth[base + k];
+                    O.delta[base + k] = first ? 0.0f : q - pv;
+                    O.prev_depth[base + k] = q;
+                }
+                if constexpr (kF16 == 1)
+                    static_cast<_Float16*>(O.depth_f16)[base + __umul24(r, az) + a] = static_cast<_Float16>(q);
+                if constexpr (kF16 == 2) tile[__umul24(a, pitch) + r] = static_cast<_Float16>(q);
+            }
             r += dr;
-            t += dt;
+            a += da;
             if (r >= el) {
                 r -= el;
-                t += wrap;
+                ++a;
             }
-            // keep the running (r, t): recomputing them from k costs integer multiplies
-            asm volatile("" : "+v"(r), "+v"(t));
+            // keep the running (a, r): recomputing them from k costs integer multiplies
+            asm volatile("" : "+v"(r), "+v"(a));
+        }
+    };
+    constexpr int32_t kStep = kThreads * kBatch;
+    int32_t b0 = 0;
+    for (; b0 + kStep <= n; b0 += kStep) run(std::integral_constant<bool, false>{}, b0);
+    if (b0 < n) run(std::integral_constant<bool, true>{}, b0);
+    for (int off = 32; off > 0; off >>= 1) mn = fminf(mn, __shfl_xor(mn, off));
+    const int32_t w = tid >> 6;
+    if ((tid & 63) == 0) {
+        uint32_t* o = red + kRed * w;
+        o[0] = n_sat;
+        o[1] = n_prox;
+        o[2] = n_band;
+        o[3] = n_fwd;
+        o[4] = n_nan;
+        o[5] = __float_as_uint(mn);
+    }
+    __syncthreads();
+    if constexpr (kF16 == 2) {
+        // Az is even: halves t and t + 1 share r, at tile[a * pitch + r] and pitch further
+        uint32_t* out = reinterpret_cast<uint32_t*>(static_cast<_Float16*>(O.depth_f16) + base);
+        const uint16_t* src = reinterpret_cast<const uint16_t*>(tile);
+        int32_t r = (2 * tid) / az;
+        int32_t a = 2 * tid - r * az;
+        const int32_t dr2 = (2 * kThreads) / az, da2 = 2 * kThreads - dr2 * az;
+        for (int32_t i = tid; i < n / 2; i += kThreads) {
+            const int32_t at = __umul24(a, pitch) + r;
+            out[i] = static_cast<uint32_t>(src[at]) | (static_cast<uint32_t>(src[at + pitch]) << 16);
+            r += dr2;
+            a += da2;
+            if (a >= az) {
+                a -= az;
+                ++r;
+            }
         }
     }
-    if (O.depth_f16 && P.stage16) {
-        __syncthreads();
-        uint32_t* out = reinterpret_cast<uint32_t*>(static_cast<_Float16*>(O.depth_f16) + base);
-        const uint32_t* src = reinterpret_cast<const uint32_t*>(lds16);
-        for (int32_t k = threadIdx.x; k < n / 2; k += kThreads) out[k] = src[k];
-    }
-    n_sat = block_sum(n_sat, lds_u);
-    n_prox = block_sum(n_prox, lds_u);
-    n_band = block_sum(n_band, lds_u);
-    n_fwd = block_sum(n_fwd, lds_u);
-    n_nan = block_sum(n_nan, lds_u);
-    mn = block_min(mn, lds_f);
-    if (n_nan != 0) mn = __builtin_nanf("");  // torch.amin: NaN if any input is NaN
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
+        uint32_t c[kRed - 1] = {0, 0, 0, 0, 0};
+        float lo = INFINITY;
+        for (int32_t v = 0; v < kThreads / 64; ++v) {
+            for (int32_t j = 0; j < kRed - 1; ++j) c[j] += red[kRed * v + j];
+            lo = fminf(lo, __uint_as_float(red[kRed * v + 5]));
+        }
+        if (c[4] != 0) lo = __builtin_nanf("");  // torch.amin: NaN if any input is NaN
         const float fn = static_cast<float>(n);
         if (O.stats) {
             float* st = O.stats + 5 * static_cast<int64_t>(e);
-            st[0] = mn;
-            st[1] = static_cast<float>(n_sat) / fn;
-            st[2] = O.proximity_threshold > 0.0f ? static_cast<float>(n_prox) / fn : 0.0f;
-            st[3] = band ? static_cast<float>(n_band) / fn : 0.0f;
-            st[4] = band ? static_cast<float>(n_fwd) / static_cast<float>(2 * fwd * el) : 0.0f;
+            st[0] = lo;
+            st[1] = static_cast<float>(c[0]) / fn;
+            st[2] = O.proximity_threshold > 0.0f ? static_cast<float>(c[1]) / fn : 0.0f;
+            st[3] = band ? static_cast<float>(c[2]) / fn : 0.0f;
+            st[4] = band ? static_cast<float>(c[3]) / static_cast<float>(2 * fwd * el) : 0.0f;
         }
-        if (O.collision) O.collision[e] = mn < O.collision_clearance ? 1 : 0;  // sdfdag_backend.py:1340
+        if (O.collision) O.collision[e] = lo < O.collision_clearance ? 1 : 0;  // sdfdag_backend.py:1340
     }
 }
 
-int launch(const PostParams& P, hipStream_t stream) {
-    const int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
-    const int64_t blocks = static_cast<int64_t>(P.env_blocks) + point_blocks;
-    if (blocks == 0) return NAVI_OK;
-    const size_t lds = P.stage16 ? static_cast<size_t>(P.O.azimuth_bins) * P.O.elevation_bins * 2 : 0;
-    hipLaunchKernelGGL(observation_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
+// Workgroups [0, point_blocks) answer point queries, one lane each; they come
+// first so that their chains of dependent record reads start with the launch.
+// The rest do the post-pass, one env each.
+template <bool kObs, bool kDelta, int kF16>
+__global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
+    if (static_cast<int32_t>(blockIdx.x) < P.point_blocks) {
+        const int32_t i = static_cast<int32_t>(blockIdx.x) * kThreads + threadIdx.x;
+        if (i < P.n_points) point_query(P, i);
+        return;
+    }
+    extern __shared__ _Float16 tile[];  // the env's fp16 tile when staged
+    __shared__ uint32_t red[kRed * (kThreads / 64)];
+    observe_env<kObs, kDelta, kF16>(P, static_cast<int32_t>(blockIdx.x) - P.point_blocks, tile, red);
+}
+
+template <bool kObs, bool kDelta, int kF16>
+int launch_as(const PostParams& P, hipStream_t stream, unsigned blocks, size_t lds) {
+    hipLaunchKernelGGL((observation_kernel<kObs, kDelta, kF16>), dim3(blocks), dim3(kThreads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;
+}
+
+template <bool kObs, bool kDelta>
+int launch_f16(const PostParams& P, hipStream_t stream, unsigned blocks, size_t lds) {
+    if (!P.O.depth_f16) return launch_as<kObs, kDelta, 0>(P, stream, blocks, lds);
+    if (P.stage16) return launch_as<kObs, kDelta, 2>(P, stream, blocks, lds);
+    return launch_as<kObs, kDelta, 1>(P, stream, blocks, lds);
+}
+
+int launch(PostParams& P, hipStream_t stream) {
+    const int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
+    const int64_t blocks = static_cast<int64_t>(P.n_envs) + point_blocks;
+    if (blocks == 0) return NAVI_OK;
+    P.point_blocks = static_cast<int32_t>(point_blocks);
+    const size_t lds = P.stage16 ? static_cast<size_t>(P.O.azimuth_bins) * P.pitch * 2 : 0;
+    const unsigned b = static_cast<unsigned>(blocks);
+    if (P.O.obs) return P.O.delta ? launch_f16<true, true>(P, stream, b, lds) : launch_f16<true, false>(P, stream, b, lds);
+    return P.O.delta ? launch_f16<false, true>(P, stream, b, lds) : launch_f16<false, false>(P, stream, b, lds);
 }
 
 int points_setup(PostParams& P, const navi_point_queries* Q) {
@@ -342,12 +413,12 @@ extern "C" int navi_observe(const navi_observation* observation, const navi_poin
         if (O.delta && !O.prev_depth) return set_error(NAVI_E_ARG, "delta needs prev_depth");
         P.O = O;
         P.n_envs = static_cast<int32_t>(O.n_envs);
-        P.env_blocks = P.n_envs;
         P.saturation = static_cast<float>(static_cast<double>(O.max_distance) - 1e-3);
         P.inv_log_denom = 1.0f / static_cast<float>(std::log1p(static_cast<double>(O.max_distance)));
-        const int64_t n = static_cast<int64_t>(O.azimuth_bins) * O.elevation_bins;
-        // a 48 KiB tile at most, and an even count for the 4-byte copy out
-        P.stage16 = (O.depth_f16 != nullptr && n % 2 == 0 && n * 2 <= 48 * 1024) ? 1 : 0;
+        // a 48 KiB tile at most, and an even Az for the 4-byte copy out
+        P.pitch = O.elevation_bins | 1;
+        P.stage16 = (O.depth_f16 != nullptr && O.azimuth_bins % 2 == 0 &&
+                     static_cast<int64_t>(O.azimuth_bins) * P.pitch * 2 <= 48 * 1024) ? 1 : 0;
     }
     const int code = points_setup(P, queries);
     if (code != NAVI_OK) return code;

@@ -210,10 +210,11 @@ def _observe_oracle_check(got, want):
 
 
 @pytest.mark.parametrize("az,el,band", [(256, 48, (1.5, 30.0)), (12, 3, (1.5, 8.0)), (7, 5, (3.0, 3.0)),
-                                         (256, 128, (1.5, 30.0))])
+                                         (256, 128, (1.5, 30.0)), (10, 1000, (1.5, 30.0)), (2, 4, (0.5, 20.0))])
 def test_observe_matches_oracle(gpu, corpus, az, el, band):
-    """(256, 48) and (12, 3) stage the fp16 tile in LDS; (7, 5) (odd count) and
-    (256, 128) (64 KiB tile) write it directly."""
+    """(256, 48), (12, 3), (10, 1000) and (2, 4) stage the fp16 tile in LDS (odd
+    row pitch 49, 3, 1001, 5; 10,000 and 8 elements end in a partial batch); (7, 5)
+    (odd Az) and (256, 128) (a 66 KB tile) write it directly."""
     import torch
 
     res = _resident(corpus)
@@ -240,6 +241,16 @@ def test_observe_matches_oracle(gpu, corpus, az, el, band):
                 out_stats=st, out_collision=co, semantics=ts, out_obs=obs, prev_depth=tprev, out_delta=delta)
     torch.cuda.synchronize()
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
+    # the same with only the fp16 depth and the statistics (the observation step's outputs),
+    # a kernel compiled without the float32 outputs
+    d16b = torch.empty_like(d16)
+    stb = torch.empty_like(st)
+    cob = torch.empty_like(co)
+    res.observe(td, az, el, 30.0, structure_band_min=band[0], structure_band_max=band[1], out_depth_f16=d16b,
+                out_stats=stb, out_collision=cob)
+    torch.cuda.synchronize()
+    assert torch.equal(d16b.view(torch.int16), d16.view(torch.int16))
+    assert torch.equal(stb.view(torch.int32), st.view(torch.int32)) and torch.equal(cob, co)
     # float32 outputs: depth within DEPTH_RTOL, semantic / valid exact
     go = obs.cpu().numpy()
     np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
