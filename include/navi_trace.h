@@ -160,10 +160,6 @@ int navi_record_depth(const uint32_t* records, uint64_t n_records, uint32_t root
 int navi_build_cell_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot, int32_t depth,
                           uint64_t* out_table);
 
-/* navi_build_cell_table at depth 4: 4096 entries. */
-int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
-                          uint64_t* out_table);
-
 /*
  * Throughput tracer over the device layout: n_envs * rays_per_env rays, env e
  * traces scenes[env_scene ? env_scene[e] : 0] (at most 1024 scenes; `records`

@@ -55,8 +55,6 @@ _u32p = ctypes.POINTER(ctypes.c_uint32)
 _lib.navi_relayout.restype = ctypes.c_int
 _lib.navi_relayout.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p, _u32p, _vp]
 _lib.navi_trace_relaid.restype = ctypes.c_int
-_lib.navi_build_root_table.restype = ctypes.c_int
-_lib.navi_build_root_table.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _vp]
 _lib.navi_build_cell_table.restype = ctypes.c_int
 _lib.navi_build_cell_table.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int32, _vp]
 _lib.navi_record_depth.restype = ctypes.c_int
@@ -135,17 +133,6 @@ def relayout(words):
     check(_lib.navi_relayout(w.ctypes.data, w.size, rec.ctypes.data, n.value, ctypes.byref(n),
                              ctypes.byref(root), levels.ctypes.data))
     return rec[: n.value], int(root.value), levels
-
-
-def root_table(records, root_slot):
-    """Host root table of one scene (``navi_build_root_table``): uint64 [4096]."""
-    import numpy as np
-
-    rec = np.ascontiguousarray(records, dtype=np.uint32).reshape(-1, 8)
-    out = np.zeros(4096, np.uint64)
-    check(_lib.navi_build_root_table(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
-                                     out.ctypes.data))
-    return out
 
 
 def cell_table(records, root_slot, depth):

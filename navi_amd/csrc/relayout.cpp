@@ -236,12 +236,6 @@ extern "C" int navi_build_cell_table(const uint32_t* records, uint64_t n_records
     return NAVI_OK;
 }
 
-// The cell table of depth 4 (4096 entries).
-extern "C" int navi_build_root_table(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
-                                     uint64_t* out_table) {
-    return navi_build_cell_table(records, n_records, root_slot, 4, out_table);
-}
-
 // Longest chain of internal records below the root, in levels: the deepest
 // record reachable from root_slot sits at that depth (the root at 0). Records
 // hold record slots as indices into `records` (a pool). *max_depth is

@@ -600,8 +600,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         }
         has_ray = has_ray && !finish;
         if (finish) {
-            P.out_d[ray] = t;
-            P.out_s[ray] = sem;
+            // non-temporal: lines of these scattered 4-byte stores do not stay in L2
+            __builtin_nontemporal_store(t, &P.out_d[ray]);
+            __builtin_nontemporal_store(sem, &P.out_s[ray]);
             if (P.out_steps) P.out_steps[ray] = step;
         }
     }
@@ -1040,8 +1041,9 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
             }
         }
         if (finish) {
-            P.out_d[ray] = t;
-            P.out_s[ray] = sem;
+            // non-temporal: lines of these scattered 4-byte stores do not stay in L2
+            __builtin_nontemporal_store(t, &P.out_d[ray]);
+            __builtin_nontemporal_store(sem, &P.out_s[ray]);
             if (P.out_steps) P.out_steps[ray] = step;
         }
     }

@@ -239,7 +239,7 @@ def _walk(rec, root, cell, depth=4):
 
 
 @pytest.mark.parametrize("case", ["room", "shallow", "malformed", "one_leaf", "offset"])
-def test_root_table_matches_record_walks(case):
+def test_depth4_cell_table_matches_record_walks(case):
     from navi_amd import scenes as S
 
     if case in ("room", "offset"):
@@ -255,7 +255,7 @@ def test_root_table_matches_record_walks(case):
     if case == "offset":  # the scene sits at record 7 of a pool
         rec = np.concatenate([np.full((7, 8), 0x7FFFFFFF, np.uint32), np.where(rec < 0x7FFFFFFD, rec + 7, rec)])
         root += 7
-    table = _native.root_table(rec, root)
+    table = _native.cell_table(rec, root, 4)
     slots = table & 0xFFFFFFFF
     depths = table >> 32
     for cell in range(4096):
@@ -273,7 +273,7 @@ def test_root_table_matches_record_walks(case):
 def test_cell_table_matches_record_walks(depth):
     """navi_build_cell_table at every depth against record walks (every cell up to
     depth 5, a seeded sample deeper), on a scene whose leaves lie at depths 5 to 7,
-    with a pool offset; at depth 4 it equals navi_build_root_table."""
+    with a pool offset."""
     from navi_amd import scenes as S
 
     rec, root, _ = _native.relayout(S.box_room(resolution=128, seed=3).compile())
@@ -281,8 +281,6 @@ def test_cell_table_matches_record_walks(depth):
     root += 5
     table = _native.cell_table(rec, root, depth)
     assert table.size == 8 ** depth
-    if depth == 4:
-        assert np.array_equal(table, _native.root_table(rec, root))
     cells = range(table.size) if depth <= 5 else np.random.default_rng(depth).integers(0, table.size, 20000)
     for cell in cells:
         slot, d = _walk(rec, root, int(cell), depth)
@@ -368,7 +366,7 @@ def test_relayout_resolves_bad_children_of_shallow_scenes(n, kept):
     assert _native.record_depth(rec, root) == n - 1
     assert bool((rec == 0x7FFFFFFD).any()) == kept
     assert bool((rec == 0x7FFFFFFE).any()) == (not kept)
-    table = _native.root_table(rec, root)
+    table = _native.cell_table(rec, root, 4)
     assert not ((table & 0xFFFFFFFF) == 0x7FFFFFFD).any()
 
 
