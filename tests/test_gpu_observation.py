@@ -343,9 +343,10 @@ def test_observation_step_end_to_end(gpu, corpus):
 
 
 def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
-    """The bench-sdfdag harness on a .gmdag file: the command runs and reports the
-    reference's summary keys, and one harness step's observation, delta and
-    statistics match the oracle pipeline on the rays that step cast."""
+    """The bench-sdfdag harness on two .gmdag files resident together: the command
+    runs and reports the reference's summary keys, and one harness step's rays,
+    observation, delta and statistics match the oracle pipeline on the poses that
+    step traced, each actor in its own scene."""
     import json as _json
 
     import torch
@@ -353,18 +354,20 @@ def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
     from navi_amd import bench_sdfdag, gmdag
     from navi_amd import scenes as S
 
-    scene = S.box_room(seed=4, resolution=64)
-    path = tmp_path / "room.gmdag"
-    gmdag.write_gmdag(path, scene.compile(), scene.resolution, scene.bbox_min_list, scene.voxel_size)
-    assert bench_sdfdag.main(["--gmdag-file", str(path), "--actors", "6", "--steps", "3", "--warmup-steps", "1",
-                              "--azimuth-bins", "32", "--elevation-bins", "8", "--json"]) == 0
+    paths = []
+    for name, scene in (("room", S.box_room(seed=4, resolution=64)), ("clutter", S.cluttered(seed=2, resolution=64))):
+        paths.append(tmp_path / f"{name}.gmdag")
+        gmdag.write_gmdag(paths[-1], scene.compile(), scene.resolution, scene.bbox_min_list, scene.voxel_size)
+    assert bench_sdfdag.main(["--gmdag-file", str(paths[0]), str(paths[1]), "--actors", "6", "--steps", "3",
+                              "--warmup-steps", "1", "--azimuth-bins", "32", "--elevation-bins", "8", "--json"]) == 0
     summary = _json.loads(capsys.readouterr().out)
     for key in ("measured_sps", "avg_batch_ms", "avg_actor_ms", "total_batches", "total_actor_steps"):
         assert key in summary
-    assert summary["total_actor_steps"] == 6 * 4
+    assert summary["total_actor_steps"] == 6 * 4 and summary["scenes"] == 2
 
-    asset = gmdag.load_gmdag_asset(path)
-    h = bench_sdfdag.ObservationHarness(asset.nodes, asset.bbox_min, asset.bbox_max, 5, 32, 8, 30.0, 128)
+    assets = [gmdag.load_gmdag_asset(p) for p in paths]
+    h = bench_sdfdag.ObservationHarness([(a.nodes, a.bbox_min, a.bbox_max) for a in assets], 5, 32, 8, 30.0, 128)
+    assert h.env_scene.cpu().tolist() == [0, 1, 0, 1, 0]
     seen = {}
     real = h.res.cast_rays_poses
 
@@ -379,13 +382,57 @@ def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
     torch.cuda.synchronize()
     dirs = _rotate(oracle.ray_directions(32, 8), seen["rot"])
     origins = np.ascontiguousarray(np.broadcast_to(seen["pos"][:, None, :], dirs.shape))
-    bmin, bmax = list(asset.bbox_min), list(asset.bbox_max)
-    ref = oracle.trace(asset.nodes, origins, dirs, 128, 30.0, bmin, bmax)
-    want = oracle.observe(ref["distance"], 32, 8, 30.0, semantics=ref["semantic"], prev_depth=prev0)
-    assert np.array_equal(h.out_d.cpu().numpy().view(np.uint32), ref["distance"].view(np.uint32))
+    dist = np.empty(dirs.shape[:2], np.float32)
+    sem = np.empty(dirs.shape[:2], np.int32)
+    for s_id, a in enumerate(assets):
+        rows = np.arange(5)[np.arange(5) % 2 == s_id]
+        r = oracle.trace(a.nodes, origins[rows], dirs[rows], 128, 30.0, list(a.bbox_min), list(a.bbox_max))
+        dist[rows], sem[rows] = r["distance"], r["semantic"]
+    want = oracle.observe(dist, 32, 8, 30.0, semantics=sem, prev_depth=prev0)
+    assert np.array_equal(h.out_d.cpu().numpy().view(np.uint32), dist.view(np.uint32))
+    assert np.array_equal(h.out_s.cpu().numpy(), sem)
     go = h.obs.cpu().numpy()
     np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
     np.testing.assert_allclose(go[:, 0], want["obs"][:, 0], rtol=DEPTH_RTOL, atol=1e-7)
     np.testing.assert_allclose(h.delta.cpu().numpy(), want["delta"], rtol=0, atol=DEPTH_RTOL)
     np.testing.assert_allclose(h.stats.cpu().numpy()[:, 1:], want["stats"][:, 1:], atol=1e-6)
+
+
+def test_bench_sdfdag_kinematics_closed_forms(gpu):
+    """The harness's kinematics against values worked out by hand from
+    sdfdag_backend.py:560-617 and config.py:94-109: full speed when the previous
+    frame's forward depth is far (log-normalised 1.0: 30 m), the 0.05 floor when it
+    is 0, velocity smoothing 0.85 / 0.15 across two steps, yaw integrated over 0.02
+    s, and the clamp to the scene box."""
+    import torch
+
+    from navi_amd import bench_sdfdag
+    from navi_amd import scenes as S
+
+    sc = S.box_room(seed=4, resolution=64)
+    h = bench_sdfdag.ObservationHarness([(sc.compile(), sc.bbox_min_list, sc.bbox_max)], 3, 32, 8, 30.0, 64)
+    lo = np.asarray(sc.bbox_min_list, np.float64)
+    mid = (lo + np.asarray(sc.bbox_max)) / 2
+    h.pos.copy_(torch.tensor([mid, mid, [mid[0], mid[1], lo[2] + 0.01]], dtype=torch.float32))
+    h.yaw.copy_(torch.tensor([0.0, math.pi / 2, 0.0]))
+    h.prev_depth.fill_(1.0)
+    h.prev_depth[1].zero_()
+    yaw0 = h.yaw.cpu().numpy().astype(np.float64)
+    h.kinematics()
+    pos1, yaw1 = h.pos.cpu().numpy().astype(np.float64), h.yaw.cpu().numpy().astype(np.float64)
+    # actor 0: factor 1, forward 1.5 * 5 = 7.5, smoothed 0.85 * 7.5 = 6.375 along -z
+    np.testing.assert_allclose(pos1[0], mid + [0.0, 0.0, -6.375 * 0.02], atol=2e-6)
+    assert abs(yaw1[0] - 0.85 * 0.15 * 3.0 * 0.02) < 1e-6
+    # actor 1: factor 0.05 (depth 0), facing -x at yaw pi/2, yaw rate -0.15 * 3
+    np.testing.assert_allclose(pos1[1], mid + [-0.85 * 7.5 * 0.05 * 0.02, 0.0, 0.0], atol=2e-6)
+    assert abs(yaw1[1] - (yaw0[1] - 0.85 * 0.15 * 3.0 * 0.02)) < 1e-6
+    # actor 2 starts 1 cm inside the -z face and moves 12.75 cm towards it: clamped to the face
+    assert pos1[2][2] == np.float32(lo[2])
+    # second step: smoothed 0.85 * 7.5 + 0.15 * 6.375 = 7.33125 along the new heading
+    h.kinematics()
+    pos2 = h.pos.cpu().numpy().astype(np.float64)
+    v = 0.85 * 7.5 + 0.15 * 6.375
+    np.testing.assert_allclose(pos2[0] - pos1[0], [-v * math.sin(yaw1[0]) * 0.02, 0.0, -v * math.cos(yaw1[0]) * 0.02],
+                               atol=2e-6)
+    np.testing.assert_allclose(h.prev_linear.cpu().numpy()[0], [v, 0.0, 0.0], rtol=1e-6)
     assert np.array_equal(h.stats.cpu().numpy()[:, 0], want["stats"][:, 0])
