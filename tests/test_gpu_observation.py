@@ -396,6 +396,7 @@ def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
     np.testing.assert_allclose(go[:, 0], want["obs"][:, 0], rtol=DEPTH_RTOL, atol=1e-7)
     np.testing.assert_allclose(h.delta.cpu().numpy(), want["delta"], rtol=0, atol=DEPTH_RTOL)
     np.testing.assert_allclose(h.stats.cpu().numpy()[:, 1:], want["stats"][:, 1:], atol=1e-6)
+    assert np.array_equal(h.stats.cpu().numpy()[:, 0], want["stats"][:, 0])
 
 
 def test_bench_sdfdag_kinematics_closed_forms(gpu):
@@ -413,7 +414,8 @@ def test_bench_sdfdag_kinematics_closed_forms(gpu):
     h = bench_sdfdag.ObservationHarness([(sc.compile(), sc.bbox_min_list, sc.bbox_max)], 3, 32, 8, 30.0, 64)
     lo = np.asarray(sc.bbox_min_list, np.float64)
     mid = (lo + np.asarray(sc.bbox_max)) / 2
-    h.pos.copy_(torch.tensor([mid, mid, [mid[0], mid[1], lo[2] + 0.01]], dtype=torch.float32))
+    start = np.array([mid, mid, [mid[0], mid[1], lo[2] + 0.01]], np.float32)
+    h.pos.copy_(torch.from_numpy(start))
     h.yaw.copy_(torch.tensor([0.0, math.pi / 2, 0.0]))
     h.prev_depth.fill_(1.0)
     h.prev_depth[1].zero_()
@@ -435,4 +437,3 @@ def test_bench_sdfdag_kinematics_closed_forms(gpu):
     np.testing.assert_allclose(pos2[0] - pos1[0], [-v * math.sin(yaw1[0]) * 0.02, 0.0, -v * math.cos(yaw1[0]) * 0.02],
                                atol=2e-6)
     np.testing.assert_allclose(h.prev_linear.cpu().numpy()[0], [v, 0.0, 0.0], rtol=1e-6)
-    assert np.array_equal(h.stats.cpu().numpy()[:, 0], want["stats"][:, 0])
