@@ -114,6 +114,7 @@ struct RelaidParams {
     uint32_t n_units;              // work units of unit_rays rays
     uint32_t unit_rays;            // 128 (2 tiles), or 64 for batches too small to fill the chip
     uint32_t small_tables;         // the cell tables span fewer than 2^32 bytes
+    uint32_t stage;                // finished rays staged per tile in LDS (fast march)
 };
 
 // Work index q -> ray id (env * R + r).
@@ -152,6 +153,19 @@ constexpr uint32_t kRefillMinFast = 12;
 // held by one wave when the queue runs dry, smaller ones cost more claims
 constexpr uint32_t kUnitRays = 128;
 constexpr uint32_t kSmallUnitRays = 64;  // one tile, for small batches
+// Output staging of the fast march: each wave keeps a ring of kStageSlots
+// tiles (64 rays) in LDS, a finished ray's distance and semantic go to its
+// tile's slot, and a slot is written out when a new tile evicts it (or the
+// wave ends): eight consecutive lanes then store eight consecutive rays, whole
+// 32-byte sectors, where a finished ray's own store writes 4 bytes of a line
+// that L2 has long evicted before the rest of its tile is done. A slot
+// position whose semantic is kStageEmpty holds no result (semantics are
+// 15-bit leaf values or 0).
+constexpr uint32_t kStageSlots = 4;
+constexpr uint32_t kStageWords = 128;  // per slot: 64 distances, then 64 semantics
+constexpr uint32_t kStageEmpty = 0xffffffffu;
+constexpr uint32_t kNoTile = 0xffffffffu;
+constexpr size_t kStageLds = 4 * kStageSlots * kStageWords * sizeof(uint32_t);  // four waves per workgroup
 
 // A scene as the kernel reads it, staged in LDS once per workgroup so a lane
 // keeps only its scene index in registers.
@@ -363,7 +377,7 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
 // offsets).
 template <int kDepth, int kPD, bool kPoses>
 __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
-                                           const float* lds_planes) {
+                                           const float* lds_planes, uint32_t* lds_stage) {
     static_assert(kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2, "planes of 4..6 levels");
     constexpr uint32_t D = kDepth;                    // the table depth
     constexpr uint32_t kAxis = axis_stride(kPD);      // floats per axis
@@ -389,6 +403,33 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     int32_t sem = 0, step = 0;
     Box lf{};
 
+    // ---- output staging: the wave's slots (kStageSlots tiles), their tiles
+    // (uniform), and per lane its ray's slot and position (bit 31 set) or 0
+    // (the ray stores its own outputs) ----
+    const bool stage = P.stage != 0u;
+    uint32_t tag = 0, ring = 0;
+    uint32_t st0 = kNoTile, st1 = kNoTile, st2 = kNoTile, st3 = kNoTile;
+    uint32_t* const my_stage = lds_stage + (threadIdx.x >> 6) * (kStageSlots * kStageWords);
+    const uint32_t flush_pos = P.tile_el ? (((lane & 7u) << 3) | (lane >> 3)) : lane;
+    // writes out slot k (tile `tile`) and empties it; every lane of the wave
+    // takes one position, eight lanes per run of eight consecutive rays
+    auto flush_slot = [&](uint32_t k, uint32_t tile) {
+        uint32_t* sl = my_stage + k * kStageWords;
+        const uint32_t sv = sl[64u + flush_pos];
+        const uint32_t tv = sl[flush_pos];
+        sl[64u + flush_pos] = kStageEmpty;
+        if (sv != kStageEmpty) {
+            int32_t env = 0;
+            const uint32_t r = ray_of(P, tile * 64u + flush_pos, env);
+            __builtin_nontemporal_store(__uint_as_float(tv), &P.out_d[r]);
+            __builtin_nontemporal_store(static_cast<int32_t>(sv), &P.out_s[r]);
+        }
+    };
+    if (stage) {
+#pragma unroll
+        for (uint32_t k = 0; k < kStageSlots; ++k) my_stage[k * kStageWords + 64u + lane] = kStageEmpty;
+    }
+
     while (true) {
         // ---- refill idle lanes (as the general march) ----
         const uint64_t need = __ballot(!has_ray);
@@ -398,7 +439,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
             const uint32_t q = claim(P, sched, n_need, rank, lane);
             RayStart R;
+            bool fresh = false;
             if (!has_ray && start_ray<kPoses>(P, q, R) == 1) {
+                fresh = true;
                 ray = R.ray;
                 scene = R.scene;
                 ox = R.ox;
@@ -421,6 +464,42 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 lf_ok = (S.root & 0x80000000u) != 0u;
                 lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
                 lf_slot = S.root;
+            }
+            if (stage) {
+                // each tile among the fresh rays (at most two per refill) gets a
+                // slot: the one holding it, else the ring's next, written out
+                // first; rays of an evicted tile still marching store their own
+                const uint32_t qtile = q >> 6;
+                uint64_t todo = __ballot(fresh);
+                while (todo != 0ull) {
+                    const uint32_t T = __builtin_amdgcn_readlane(qtile, static_cast<uint32_t>(__builtin_ctzll(todo)));
+                    uint32_t k;
+                    if (st0 == T) {
+                        k = 0;
+                    } else if (st1 == T) {
+                        k = 1;
+                    } else if (st2 == T) {
+                        k = 2;
+                    } else if (st3 == T) {
+                        k = 3;
+                    } else {
+                        k = ring;
+                        ring = (ring + 1u) & (kStageSlots - 1u);
+                        const uint32_t old = k == 0 ? st0 : (k == 1 ? st1 : (k == 2 ? st2 : st3));
+                        if (old != kNoTile) {
+                            flush_slot(k, old);
+                            const bool evicted = (tag >> 31) != 0u && ((tag >> 6) & 3u) == k;
+                            tag = evicted ? 0u : tag;
+                        }
+                        st0 = k == 0 ? T : st0;
+                        st1 = k == 1 ? T : st1;
+                        st2 = k == 2 ? T : st2;
+                        st3 = k == 3 ? T : st3;
+                    }
+                    const bool same = fresh && qtile == T;
+                    tag = same ? (0x80000000u | (k << 6) | (q & 63u)) : tag;
+                    todo &= ~__ballot(same);
+                }
             }
         }
         if (__ballot(has_ray) == 0ull) {
@@ -600,11 +679,23 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         }
         has_ray = has_ray && !finish;
         if (finish) {
-            // non-temporal: lines of these scattered 4-byte stores do not stay in L2
-            __builtin_nontemporal_store(t, &P.out_d[ray]);
-            __builtin_nontemporal_store(sem, &P.out_s[ray]);
+            if ((tag >> 31) != 0u) {
+                uint32_t* e = my_stage + ((tag >> 6) & 3u) * kStageWords + (tag & 63u);
+                e[0] = __float_as_uint(t);
+                e[64] = static_cast<uint32_t>(sem);
+            } else {
+                // non-temporal: lines of these scattered 4-byte stores do not stay in L2
+                __builtin_nontemporal_store(t, &P.out_d[ray]);
+                __builtin_nontemporal_store(sem, &P.out_s[ray]);
+            }
             if (P.out_steps) P.out_steps[ray] = step;
         }
+    }
+    if (stage) {
+        if (st0 != kNoTile) flush_slot(0, st0);
+        if (st1 != kNoTile) flush_slot(1, st1);
+        if (st2 != kNoTile) flush_slot(2, st2);
+        if (st3 != kNoTile) flush_slot(3, st3);
     }
 }
 
@@ -1108,7 +1199,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     }
     if constexpr (kPlanes) {
         if (planes && tame && shallow && !void_cache && P.small_tables)
-            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes);
+            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
+                                            reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * kScene));
         else
             march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
     } else {
@@ -1246,7 +1338,12 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
         }
         if (pd) break;
     }
-    const size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (pd ? scene_stride(pd) * sizeof(float) : 0));
+    size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (pd ? scene_stride(pd) * sizeof(float) : 0));
+    // output staging where it fits the budget the planes were sized for (and
+    // no step counts are asked for: those are stored per ray)
+    P.stage = (pd != 0 && P.out_steps == nullptr && lds + kStageLds <= (lds <= kPlaneLds ? kPlaneLds : kPlaneLdsWide))
+                  ? 1u : 0u;
+    if (P.stage) lds += kStageLds;
     const bool poses = P.local_dirs != nullptr;
     void (*kernel)(RelaidParams) = nullptr;
 #define NAVI_RELAID(d, p) (poses ? trace_relaid_kernel<d, p, true> : trace_relaid_kernel<d, p, false>)
