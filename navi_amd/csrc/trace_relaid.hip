@@ -49,6 +49,16 @@
 #include "navi_trace.h"
 #include "trace_common.hpp"
 
+// Structured buffer loads (the index scaled by the resource's stride in the
+// address unit): the LLVM intrinsics, which clang exposes only in their raw form.
+extern "C" __device__ uint32_t navi_struct_load_b32(__amdgpu_buffer_rsrc_t rsrc, int32_t index, int32_t voffset,
+                                                     int32_t soffset, int32_t aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.i32");
+typedef uint32_t navi_u32x2 __attribute__((ext_vector_type(2)));
+extern "C" __device__ navi_u32x2 navi_struct_load_b64(__amdgpu_buffer_rsrc_t rsrc, int32_t index, int32_t voffset,
+                                                       int32_t soffset, int32_t aux)
+    __asm("llvm.amdgcn.struct.ptr.buffer.load.v2i32");
+
 namespace navi {
 
 int set_error(int code, const char* fmt, ...);
@@ -386,11 +396,12 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     constexpr uint32_t kShP = kPD - kPrefixDepth;     // depth-kPD index >> kShP = depth-4 index
     constexpr uint32_t kShD = D - kPrefixDepth;       // depth-D index >> kShD = depth-4 index
     const uint32_t lane = threadIdx.x & 63u;
+    // indexed by slot (4 bytes) and by table entry (8 bytes)
     const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(P.records), static_cast<short>(0), static_cast<int>(P.n_records * 32u), 0x00020000);
+        const_cast<uint32_t*>(P.records), static_cast<short>(4), static_cast<int>(P.n_records * 8u), 0x00020000);
     const __amdgpu_buffer_rsrc_t tables = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint64_t*>(P.cell_table), static_cast<short>(0),
-        static_cast<int>(static_cast<uint32_t>(P.n_scenes) << (3u * D + 3u)), 0x00020000);
+        const_cast<uint64_t*>(P.cell_table), static_cast<short>(8),
+        static_cast<int>(static_cast<uint32_t>(P.n_scenes) << (3u * D)), 0x00020000);
     Sched sched = sched_init(P);
 
     // per-lane ray state; the prefix cache as in the general march's plane
@@ -576,8 +587,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 jz = append_bit(jz, gz);
             }
             // ---- one cell-table read: the slot D levels down, and its depth ----
-            const auto e = __builtin_amdgcn_raw_buffer_load_b64(
-                tables, (((((scene << D) | jz) << D | jy) << D) | jx) << 3, 0, 0);
+            const navi_u32x2 e = navi_struct_load_b64(
+                tables, static_cast<int32_t>((((((scene << D) | jz) << D | jy) << D) | jx)), 0, 0, 0);
             slot = e[0];
             const uint32_t depth = e[1];
             if (depth < D) {
@@ -617,7 +628,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             uint32_t cur_rec = slot;
             bool deeper = slot < kSlotBadChild;
             for (uint32_t trip = D; deeper && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
-                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
+                slot = navi_struct_load_b32(records, static_cast<int32_t>(descend_index(px, py, pz, cur, cur_rec)), 0, 0, 0);
                 cur_rec = slot;
                 deeper = slot < kSlotBadChild;
             }
@@ -718,11 +729,12 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
     constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
     constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
     const uint32_t lane = threadIdx.x & 63u;
-    // The record pool as a buffer resource: 32-bit byte offsets, and the
-    // hardware bounds every read by the pool's size (at most 2^27 records,
-    // 4 GiB). Dword 3 = 0x00020000: 32-bit data format, as gfx9 raw buffers need.
+    // The record pool as a buffer resource indexed by slot (stride 4 bytes): the
+    // hardware scales the index and bounds every read by the pool's size (at
+    // most 2^27 records, 2^30 slots; an out-of-range read returns 0). Dword 3 =
+    // 0x00020000: 32-bit data format, as gfx9 buffers need.
     const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(P.records), static_cast<short>(0), static_cast<int>(P.n_records * 32u), 0x00020000);
+        const_cast<uint32_t*>(P.records), static_cast<short>(4), static_cast<int>(P.n_records * 8u), 0x00020000);
     Sched sched = sched_init(P);
 
     // per-lane ray state
@@ -1009,14 +1021,14 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
             // behind a zeroed descriptor), which then ends like the 32-level
             // limit (stale result) instead of looping.
             for (uint32_t trip = D; descending && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
-                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
+                slot = navi_struct_load_b32(records, static_cast<int32_t>(descend_index(px, py, pz, cur, cur_rec)), 0, 0, 0);
                 cur_rec = slot;  // read again only while internal
                 descending = slot < kSlotBadChild;
             }
             descending = false;
         } else {
             while (descending) {
-                slot = __builtin_amdgcn_raw_buffer_load_b32(records, descend_index(px, py, pz, cur, cur_rec) << 2, 0, 0);
+                slot = navi_struct_load_b32(records, static_cast<int32_t>(descend_index(px, py, pz, cur, cur_rec)), 0, 0, 0);
                 depth += 1;
                 cur_rec = slot;
                 descending = slot < kSlotBadChild && depth < kMaxDepth;
