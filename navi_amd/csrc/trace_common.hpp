@@ -71,10 +71,22 @@ __device__ __forceinline__ uint32_t descend_octant(float px, float py, float pz,
     return oct;
 }
 
+// The wave's lanes for which b holds. (HIP's __ballot takes an int and compares
+// it with 0, which costs a select and a compare for a bool that lives as a lane
+// mask, e.g. across loop iterations.)
+__device__ __forceinline__ uint64_t wave_mask(bool b) { return __builtin_amdgcn_ballot_w64(b); }
+
+// set bits of a wave mask, as a 32-bit count (two scalar bit counts; a 64-bit
+// count would be compared on the vector unit)
+__device__ __forceinline__ uint32_t lane_count(uint64_t m) {
+    return static_cast<uint32_t>(__builtin_popcount(static_cast<uint32_t>(m))) +
+           static_cast<uint32_t>(__builtin_popcount(static_cast<uint32_t>(m >> 32)));
+}
+
 // i * 2 + b in one add-with-carry, the comparison's lane mask as carry-in
 // (the compiler spends two operations, a select and a shift-or).
 __device__ __forceinline__ uint32_t append_bit(uint32_t i, bool b) {
-    const uint64_t mask = __ballot(b);  // this lane's bit is b; inactive lanes are ignored
+    const uint64_t mask = wave_mask(b);  // this lane's bit is b; inactive lanes are ignored
     uint32_t r;
     uint64_t carry_out;
     asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(i), "s"(mask));

@@ -409,6 +409,10 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     // x | y << 8 | z << 16, all ones when nothing is cached)
     bool has_ray = false, lf_ok = false;
     uint32_t ray = 0, scene = 0, lf_slot = 0, pre_cell = 0xffffffffu;
+    // the lane's scene in LDS: its table entry and its split planes (set at a refill)
+    const SceneLds* my_scene = lds_scenes;
+    const float* my_planes = lds_planes;
+    uint32_t my_table = 0;  // the scene's first cell-table entry
     float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
     float t = 0.f, dist = 0.f;
     int32_t sem = 0, step = 0;
@@ -441,10 +445,13 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         for (uint32_t k = 0; k < kStageSlots; ++k) my_stage[k * kStageWords + 64u + lane] = kStageEmpty;
     }
 
+    // the wave's lanes without a ray, kept as a wave mask (uniform) alongside the
+    // lanes' has_ray: a ballot of a bool carried across iterations costs a select
+    // and a compare, one of a comparison in the same iteration nothing
+    uint64_t need = ~0ull;
     while (true) {
         // ---- refill idle lanes (as the general march) ----
-        const uint64_t need = __ballot(!has_ray);
-        const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
+        const uint32_t n_need = lane_count(need);
         if ((n_need >= kRefillMinFast || n_need == 64u) && !sched.exhausted) {
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
@@ -471,17 +478,22 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 pre_cell = 0xffffffffu;
                 has_ray = true;
                 // a one-leaf DAG: its leaf and the domain box (kernel.cu:139-152)
-                const SceneLds& S = lds_scenes[scene];
+                my_scene = lds_scenes + scene;
+                my_planes = lds_planes + __umul24(scene, kScene);
+                my_table = scene << (3u * D);
+                const SceneLds& S = *my_scene;
                 lf_ok = (S.root & 0x80000000u) != 0u;
                 lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
                 lf_slot = S.root;
             }
+            const uint64_t started = wave_mask(fresh);
+            need &= ~started;
             if (stage) {
                 // each tile among the fresh rays (at most two per refill) gets a
                 // slot: the one holding it, else the ring's next, written out
                 // first; rays of an evicted tile still marching store their own
                 const uint32_t qtile = q >> 6;
-                uint64_t todo = __ballot(fresh);
+                uint64_t todo = started;
                 while (todo != 0ull) {
                     const uint32_t T = __builtin_amdgcn_readlane(qtile, static_cast<uint32_t>(__builtin_ctzll(todo)));
                     uint32_t k;
@@ -509,18 +521,18 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                     }
                     const bool same = fresh && qtile == T;
                     tag = same ? (0x80000000u | (k << 6) | (q & 63u)) : tag;
-                    todo &= ~__ballot(same);
+                    todo &= ~wave_mask(same);
                 }
             }
         }
-        if (__ballot(has_ray) == 0ull) {
+        if (need == ~0ull) {
             if (sched.exhausted) break;
             continue;
         }
 
         // ---- start the step: domain and leaf-cache tests (kernel.cu:108-118) ----
-        step += has_ray ? 1 : 0;
-        const SceneLds& S = lds_scenes[scene];
+        ++step;  // a lane without a ray counts too: a refill resets its count
+        const SceneLds& S = *my_scene;
         const Box dom{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
         const float px = __builtin_fmaf(t, dx, ox);
         const float py = __builtin_fmaf(t, dy, oy);
@@ -535,7 +547,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
 
         if (descending) {
             // ---- the depth-kPD cell from the split planes ----
-            const float* hdr = lds_planes + __umul24(scene, kScene);
+            const float* hdr = my_planes;
             const float* plx = hdr + kPlaneHeader;
             const float* ply = plx + kAxis;
             const float* plz = ply + kAxis;
@@ -588,7 +600,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             }
             // ---- one cell-table read: the slot D levels down, and its depth ----
             const navi_u32x2 e = navi_struct_load_b64(
-                tables, static_cast<int32_t>((((((scene << D) | jz) << D | jy) << D) | jx)), 0, 0, 0);
+                tables, static_cast<int32_t>(my_table | (jz << (2u * D)) | (jy << D) | jx), 0, 0, 0);
             slot = e[0];
             const uint32_t depth = e[1];
             if (depth < D) {
@@ -689,6 +701,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             run = run && !fin2;
         }
         has_ray = has_ray && !finish;
+        need |= wave_mask(finish);
         if (finish) {
             if ((tag >> 31) != 0u) {
                 uint32_t* e = my_stage + ((tag >> 6) & 3u) * kStageWords + (tag & 63u);
@@ -761,8 +774,8 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
         // ---- refill lanes without a ray from the wave's chunk sequence ----
         // Refill once an eighth of the wave is idle (or all of it): the refill
         // block costs the whole wave, idle lanes only their own slot.
-        const uint64_t need = __ballot(!has_ray);
-        const uint32_t n_need = static_cast<uint32_t>(__popcll(need));
+        const uint64_t need = wave_mask(!has_ray);
+        const uint32_t n_need = lane_count(need);
         if ((n_need >= kRefillMin || n_need == 64u) && !sched.exhausted) {
             // idle lanes below this one (mbcnt: set bits of `need` under the lane)
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
@@ -800,7 +813,7 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
                 }
             }
         }
-        if (__ballot(has_ray) == 0ull) {
+        if (wave_mask(has_ray) == 0ull) {
             if (sched.exhausted) break;
             continue;
         }
