@@ -152,6 +152,18 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
     return __builtin_fmaf(e, r, q0);
 }
 
+// v with its sign flipped where d's sign bit is set (exact): a coordinate in
+// the frame mirrored along each axis on which the ray moves towards -inf
+__device__ __forceinline__ float mirror(float v, float d) {
+    return __uint_as_float(__float_as_uint(v) ^ (__float_as_uint(d) & 0x80000000u));
+}
+
+// The face of [lo, hi] ahead of a ray moving along d, in the mirrored frame:
+// hi where d's sign bit is clear, -lo where it is set.
+__device__ __forceinline__ float ahead(float lo, float hi, float d) {
+    return __float_as_int(d) < 0 ? -lo : hi;
+}
+
 constexpr uint32_t kRefillMin = 8;
 constexpr uint32_t kLeafRun = 1;  // leaf-cache steps taken after a leaf step
 // The fast march's: its step costs fewer operations, so a lane waits less on
@@ -407,16 +419,30 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     // per-lane ray state; the prefix cache as in the general march's plane
     // kernels (depth-kPD plane index of the cached cell's upper face per axis,
     // x | y << 8 | z << 16, all ones when nothing is cached)
-    bool has_ray = false, lf_ok = false;
+    //
+    // The samples are taken in a frame mirrored along each axis on which the
+    // ray's direction has its sign bit set: q' = fma(t, |d|, o') with o' the
+    // mirrored origin is -q there and q elsewhere, bit for bit (rounding is
+    // symmetric), and the sample p itself is q' with the sign flipped back. In
+    // these launches t never decreases (leaf distances are non-negative, void
+    // and domain steps positive), so along each axis the samples move one way,
+    // and a box that held an earlier sample can only be left through the faces
+    // ahead of the ray: the leaf cache and the domain test keep those faces
+    // alone (mirrored, so a sample is inside while q' <= face' on every axis).
+    // The domain's faces behind the ray hold from the origin on; a ray whose
+    // origin lies outside the domain gets NaN faces (never inside), and its
+    // first step ends it, as any step outside does while the range is below
+    // the outside-domain distance (the launch's condition for this march).
+    bool has_ray = false;
     uint32_t ray = 0, scene = 0, lf_slot = 0, pre_cell = 0xffffffffu;
-    // the lane's scene in LDS: its table entry and its split planes (set at a refill)
-    const SceneLds* my_scene = lds_scenes;
+    // the lane's scene in LDS: its split planes and first cell-table entry (set at a refill)
     const float* my_planes = lds_planes;
-    uint32_t my_table = 0;  // the scene's first cell-table entry
+    uint32_t my_table = 0;
     float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
     float t = 0.f, dist = 0.f;
     int32_t sem = 0, step = 0;
-    Box lf{};
+    // faces ahead (mirrored) of the cached leaf (NaN: none) and of the domain
+    float lfx = __builtin_nanf(""), lfy = lfx, lfz = lfx, dmx = lfx, dmy = lfx, dmz = lfx;
 
     // ---- output staging: the wave's slots (kStageSlots tiles), their tiles
     // (uniform), and per lane its ray's slot and position (bit 31 set) or 0
@@ -462,9 +488,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 fresh = true;
                 ray = R.ray;
                 scene = R.scene;
-                ox = R.ox;
-                oy = R.oy;
-                oz = R.oz;
+                ox = mirror(R.ox, R.dx);
+                oy = mirror(R.oy, R.dy);
+                oz = mirror(R.oz, R.dz);
                 dx = R.dx;
                 dy = R.dy;
                 dz = R.dz;
@@ -477,13 +503,20 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 step = 0;
                 pre_cell = 0xffffffffu;
                 has_ray = true;
-                // a one-leaf DAG: its leaf and the domain box (kernel.cu:139-152)
-                my_scene = lds_scenes + scene;
                 my_planes = lds_planes + __umul24(scene, kScene);
                 my_table = scene << (3u * D);
-                const SceneLds& S = *my_scene;
-                lf_ok = (S.root & 0x80000000u) != 0u;
-                lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                const SceneLds& S = lds_scenes[scene];
+                const Box dom{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
+                const float nan = __builtin_nanf("");
+                const bool inside = in_box(R.ox, R.oy, R.oz, dom);
+                dmx = inside ? ahead(dom.x0, dom.x1, dx) : nan;
+                dmy = inside ? ahead(dom.y0, dom.y1, dy) : nan;
+                dmz = inside ? ahead(dom.z0, dom.z1, dz) : nan;
+                // a one-leaf DAG: its leaf is the domain (kernel.cu:139-152)
+                const bool root_leaf = (S.root & 0x80000000u) != 0u;
+                lfx = root_leaf ? dmx : nan;
+                lfy = root_leaf ? dmy : nan;
+                lfz = root_leaf ? dmz : nan;
                 lf_slot = S.root;
             }
             const uint64_t started = wave_mask(fresh);
@@ -532,20 +565,20 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
 
         // ---- start the step: domain and leaf-cache tests (kernel.cu:108-118) ----
         ++step;  // a lane without a ray counts too: a refill resets its count
-        const SceneLds& S = *my_scene;
-        const Box dom{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
-        const float px = __builtin_fmaf(t, dx, ox);
-        const float py = __builtin_fmaf(t, dy, oy);
-        const float pz = __builtin_fmaf(t, dz, oz);
-        const bool in_dom = in_box(px, py, pz, dom);
-        const bool in_lf = in_box(px, py, pz, lf);
+        const float qx = __builtin_fmaf(t, fabsf(dx), ox);
+        const float qy = __builtin_fmaf(t, fabsf(dy), oy);
+        const float qz = __builtin_fmaf(t, fabsf(dz), oz);
+        const bool in_dom = qx <= dmx && qy <= dmy && qz <= dmz;
+        const bool hit_lf = qx <= lfx && qy <= lfy && qz <= lfz;  // the leaf lies in the domain
         const bool outside = !in_dom;
-        const bool hit_lf = in_dom && lf_ok && in_lf;
         const bool descending = has_ray && in_dom && !hit_lf;
-        Box cur = dom;
+        // the faces ahead (mirrored) of the box a descent ends in
+        float hx = qx, hy = qy, hz = qz;
         uint32_t slot = 0;  // an internal slot: no outcome for lanes that do not descend
 
         if (descending) {
+            const float px = mirror(qx, dx), py = mirror(qy, dy), pz = mirror(qz, dz);
+            Box cur;
             // ---- the depth-kPD cell from the split planes ----
             const float* hdr = my_planes;
             const float* plx = hdr + kPlaneHeader;
@@ -644,6 +677,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 cur_rec = slot;
                 deeper = slot < kSlotBadChild;
             }
+            hx = ahead(cur.x0, cur.x1, dx);
+            hy = ahead(cur.y0, cur.y1, dy);
+            hz = ahead(cur.z0, cur.z1, dz);
         }
 
         // ---- the query's outcome and the leaf cache ----
@@ -651,20 +687,19 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const bool new_void = slot == kSlotVoid;
         const bool is_fault = slot == kSlotFault;
         const bool is_leaf = hit_lf || new_leaf;
-        lf.x0 = new_leaf ? cur.x0 : lf.x0;
-        lf.y0 = new_leaf ? cur.y0 : lf.y0;
-        lf.z0 = new_leaf ? cur.z0 : lf.z0;
-        lf.x1 = new_leaf ? cur.x1 : lf.x1;
-        lf.y1 = new_leaf ? cur.y1 : lf.y1;
-        lf.z1 = new_leaf ? cur.z1 : lf.z1;
+        lfx = new_leaf ? hx : lfx;
+        lfy = new_leaf ? hy : lfy;
+        lfz = new_leaf ? hz : lfz;
         lf_slot = new_leaf ? slot : lf_slot;
-        lf_ok = lf_ok || new_leaf;
 
         // ---- finish the step (kernel.cu:54-85, 297-308) ----
-        const float nx = (dx > 0.f ? cur.x1 : cur.x0) - px;
-        const float ny = (dy > 0.f ? cur.y1 : cur.y0) - py;
-        const float nz = (dz > 0.f ? cur.z1 : cur.z0) - pz;
-        const float e = fminf(fminf(fminf(markstein(nx, dx, rx), markstein(ny, dy, ry)), markstein(nz, dz, rz)),
+        // The exit quotient (face - p) / d of the reference's face (hi when
+        // d > 0, else lo) is (face' - q') / |d| bit for bit: where d's sign
+        // bit is set both numerator and divisor are negated (and where
+        // d = +0 the reciprocal is NaN, so which face is moot).
+        const float nx = hx - qx, ny = hy - qy, nz = hz - qz;
+        const float e = fminf(fminf(fminf(markstein(nx, fabsf(dx), fabsf(rx)), markstein(ny, fabsf(dy), fabsf(ry))),
+                                    markstein(nz, fabsf(dz), fabsf(rz))),
                               kOutsideDomain);
         const float void_d = e > kVoidAdvanceEps ? e : kVoidAdvanceEps;  // fmaxf: e is never NaN
         const float leaf_d = half_to_float(lf_slot & 0xffffu);
@@ -687,10 +722,10 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         bool run = live && is_leaf;
 #pragma unroll
         for (uint32_t k = 0; k < kLeafRunFast; ++k) {
-            const float qx = __builtin_fmaf(t, dx, ox);
-            const float qy = __builtin_fmaf(t, dy, oy);
-            const float qz = __builtin_fmaf(t, dz, oz);
-            const bool in_lf2 = in_box(qx, qy, qz, lf);
+            const float ux = __builtin_fmaf(t, fabsf(dx), ox);
+            const float uy = __builtin_fmaf(t, fabsf(dy), oy);
+            const float uz = __builtin_fmaf(t, fabsf(dz), oz);
+            const bool in_lf2 = ux <= lfx && uy <= lfy && uz <= lfz;
             run = run && in_lf2;
             step += run ? 1 : 0;
             t = run ? t + dist : t;
@@ -1223,7 +1258,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         planes = __syncthreads_and(planes);
     }
     if constexpr (kPlanes) {
-        if (planes && tame && shallow && !void_cache && P.small_tables)
+        if (planes && tame && shallow && !void_cache && P.small_tables && P.max_distance < kOutsideDomain)
             march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
                                             reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * kScene));
         else

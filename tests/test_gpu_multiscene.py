@@ -128,6 +128,50 @@ def test_relaid_random_rays_and_short_budgets(gpu, corpus):
         _compare(_run(res, env_scene, o, d, max_steps, 45.0), ref, 45.0, f"random/{max_steps}")
 
 
+@pytest.mark.parametrize("max_distance", [30.0, 999.0, 1000.0, 1500.0])
+def test_relaid_signed_zero_axes_and_long_ranges(gpu, corpus, max_distance):
+    """The fast march samples in a frame mirrored along each axis whose direction
+    component has its sign bit set, keeps only the faces ahead of a ray (its
+    samples move one way along each axis) and ends a ray at its first step
+    outside the domain; it runs while the range lies below the outside-domain
+    distance (1000), the general march from there on. Direction components of +0
+    and -0 (axis-aligned rays, rays in coordinate planes), origins inside, outside
+    and exactly on the faces of the domains, ranges on both sides of 1000: against
+    the oracle."""
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    rng = np.random.default_rng(int(max_distance))
+    n_env, rays = 8, 640
+    env_scene = (np.arange(n_env) % len(corpus)).astype(np.int32)
+    lo = np.array([corpus[s].bbox_min_list for s in env_scene], np.float32)
+    hi = np.array([corpus[s].bbox_max for s in env_scene], np.float32)
+    span = hi - lo
+    o = rng.uniform(lo[:, None, :] - 0.05 * span[:, None, :], hi[:, None, :] + 0.05 * span[:, None, :],
+                    (n_env, rays, 3)).astype(np.float32)
+    free = np.stack([corpus[s].free_origins(rng, 1)[0] for s in env_scene]).astype(np.float32)
+    o[:, :320] = free[:, None, :]
+    # origins on a face: one coordinate exactly a domain bound
+    for k in range(320, 400):
+        axis, side = k % 3, (k // 3) % 2
+        o[:, k, axis] = (hi if side else lo)[:, axis]
+    d = rng.normal(size=(n_env, rays, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    # signed zeros: one or two components +0 or -0, and axis-aligned rays
+    for k in range(0, rays, 4):
+        axis = (k // 4) % 3
+        d[:, k, axis] = np.float32(-0.0) if (k // 12) % 2 else np.float32(0.0)
+        if k % 8 == 0:
+            other = (axis + 1) % 3
+            d[:, k, other] = np.float32(0.0) if (k // 24) % 2 else np.float32(-0.0)
+    assert np.signbit(d[d == 0]).any() and (~np.signbit(d[d == 0])).any()
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, o, d, 200, max_distance)
+    _compare(_run(res, env_scene, o, d, 200, max_distance), ref, max_distance, f"zeros/{max_distance}")
+    _compare(_run(res, env_scene, o, d, 200, max_distance, elevation_bins=16), ref, max_distance,
+             f"zeros/{max_distance}/tiles")
+
+
 def test_unknown_scene_id_reports_nan(gpu, corpus):
     from navi_amd.multiscene import ResidentScenes
 
