@@ -93,6 +93,17 @@ __device__ __forceinline__ uint32_t append_bit(uint32_t i, bool b) {
     return r;
 }
 
+// This lane's bit of a wave mask (the mask itself is the lane predicate).
+__device__ __forceinline__ bool lane_in(uint64_t mask) { return __builtin_amdgcn_inverse_ballot_w64(mask); }
+
+// i + (this lane's bit of mask): one add-with-carry, the mask as carry-in.
+__device__ __forceinline__ int32_t add_lane_bit(int32_t i, uint64_t mask) {
+    int32_t r;
+    uint64_t carry_out;
+    asm("v_addc_co_u32_e64 %0, %1, %2, 0, %3" : "=v"(r), "=s"(carry_out) : "v"(i), "s"(mask));
+    return r;
+}
+
 // descend_octant fused with slot addressing: returns base * 8 + octant, the
 // octant's z, y and x bits appended in that order (one add-with-carry each).
 __device__ __forceinline__ uint32_t descend_index(float px, float py, float pz, Box& cur, uint32_t base) {

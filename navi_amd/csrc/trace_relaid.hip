@@ -433,14 +433,13 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     // origin lies outside the domain gets NaN faces (never inside), and its
     // first step ends it, as any step outside does while the range is below
     // the outside-domain distance (the launch's condition for this march).
-    bool has_ray = false;
     uint32_t ray = 0, scene = 0, lf_slot = 0, pre_cell = 0xffffffffu;
     // the lane's scene in LDS: its split planes and first cell-table entry (set at a refill)
     const float* my_planes = lds_planes;
     uint32_t my_table = 0;
     float ox = 0.f, oy = 0.f, oz = 0.f, dx = 0.f, dy = 0.f, dz = 0.f, rx = 0.f, ry = 0.f, rz = 0.f;
-    float t = 0.f, dist = 0.f;
-    int32_t sem = 0, step = 0;
+    float t = 0.f;
+    int32_t step = 0;
     // faces ahead (mirrored) of the cached leaf (NaN: none) and of the domain
     float lfx = __builtin_nanf(""), lfy = lfx, lfz = lfx, dmx = lfx, dmy = lfx, dmz = lfx;
 
@@ -471,10 +470,14 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         for (uint32_t k = 0; k < kStageSlots; ++k) my_stage[k * kStageWords + 64u + lane] = kStageEmpty;
     }
 
-    // the wave's lanes without a ray, kept as a wave mask (uniform) alongside the
-    // lanes' has_ray: a ballot of a bool carried across iterations costs a select
-    // and a compare, one of a comparison in the same iteration nothing
+    // the wave's lanes without a ray as a wave mask (uniform); a lane reads its
+    // own bit with an inverse ballot (the mask is the lane predicate itself):
+    // a bool carried across iterations would cost a select and a compare
+    // per ballot
     uint64_t need = ~0ull;
+    // per axis the lanes whose direction has its sign bit set (the mirrored
+    // axes), as wave masks read back with inverse ballots (set at a refill)
+    uint64_t neg_x = 0, neg_y = 0, neg_z = 0;
     while (true) {
         // ---- refill idle lanes (as the general march) ----
         const uint32_t n_need = lane_count(need);
@@ -484,7 +487,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             const uint32_t q = claim(P, sched, n_need, rank, lane);
             RayStart R;
             bool fresh = false;
-            if (!has_ray && start_ray<kPoses>(P, q, R) == 1) {
+            if (__builtin_amdgcn_inverse_ballot_w64(need) && start_ray<kPoses>(P, q, R) == 1) {
                 fresh = true;
                 ray = R.ray;
                 scene = R.scene;
@@ -498,11 +501,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 ry = R.ry;
                 rz = R.rz;
                 t = 0.f;
-                dist = 0.f;
-                sem = 0;
                 step = 0;
                 pre_cell = 0xffffffffu;
-                has_ray = true;
                 my_planes = lds_planes + __umul24(scene, kScene);
                 my_table = scene << (3u * D);
                 const SceneLds& S = lds_scenes[scene];
@@ -520,6 +520,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 lf_slot = S.root;
             }
             const uint64_t started = wave_mask(fresh);
+            neg_x = wave_mask(__float_as_int(dx) < 0);
+            neg_y = wave_mask(__float_as_int(dy) < 0);
+            neg_z = wave_mask(__float_as_int(dz) < 0);
             need &= ~started;
             if (stage) {
                 // each tile among the fresh rays (at most two per refill) gets a
@@ -564,14 +567,19 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         }
 
         // ---- start the step: domain and leaf-cache tests (kernel.cu:108-118) ----
+        // The step's conditions are kept as wave masks: ballots of single
+        // comparisons (free: a comparison writes its lane mask) combined on the
+        // scalar unit, read back per lane with inverse ballots. A ballot of a
+        // combined or carried bool would cost a select and a compare each.
+        const uint64_t m_ray = ~need;
         ++step;  // a lane without a ray counts too: a refill resets its count
         const float qx = __builtin_fmaf(t, fabsf(dx), ox);
         const float qy = __builtin_fmaf(t, fabsf(dy), oy);
         const float qz = __builtin_fmaf(t, fabsf(dz), oz);
-        const bool in_dom = qx <= dmx && qy <= dmy && qz <= dmz;
-        const bool hit_lf = qx <= lfx && qy <= lfy && qz <= lfz;  // the leaf lies in the domain
-        const bool outside = !in_dom;
-        const bool descending = has_ray && in_dom && !hit_lf;
+        const uint64_t m_dom = wave_mask(qx <= dmx) & wave_mask(qy <= dmy) & wave_mask(qz <= dmz);
+        // (the leaf lies in the domain)
+        const uint64_t m_hit_lf = wave_mask(qx <= lfx) & wave_mask(qy <= lfy) & wave_mask(qz <= lfz);
+        const bool descending = lane_in(m_ray & m_dom & ~m_hit_lf);
         // the faces ahead (mirrored) of the box a descent ends in
         float hx = qx, hy = qy, hz = qz;
         uint32_t slot = 0;  // an internal slot: no outcome for lanes that do not descend
@@ -677,16 +685,15 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 cur_rec = slot;
                 deeper = slot < kSlotBadChild;
             }
-            hx = ahead(cur.x0, cur.x1, dx);
-            hy = ahead(cur.y0, cur.y1, dy);
-            hz = ahead(cur.z0, cur.z1, dz);
+            hx = __builtin_amdgcn_inverse_ballot_w64(neg_x) ? -cur.x0 : cur.x1;
+            hy = __builtin_amdgcn_inverse_ballot_w64(neg_y) ? -cur.y0 : cur.y1;
+            hz = __builtin_amdgcn_inverse_ballot_w64(neg_z) ? -cur.z0 : cur.z1;
         }
 
         // ---- the query's outcome and the leaf cache ----
-        const bool new_leaf = (slot & 0x80000000u) != 0u;
-        const bool new_void = slot == kSlotVoid;
-        const bool is_fault = slot == kSlotFault;
-        const bool is_leaf = hit_lf || new_leaf;
+        const uint64_t m_new_leaf = wave_mask(static_cast<int32_t>(slot) < 0);
+        const uint64_t m_leaf = m_hit_lf | m_new_leaf;
+        const bool new_leaf = lane_in(m_new_leaf);
         lfx = new_leaf ? hx : lfx;
         lfy = new_leaf ? hy : lfy;
         lfz = new_leaf ? hz : lfz;
@@ -704,40 +711,41 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const float void_d = e > kVoidAdvanceEps ? e : kVoidAdvanceEps;  // fmaxf: e is never NaN
         const float leaf_d = half_to_float(lf_slot & 0xffffu);
         const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
-        dist = new_void ? void_d : (is_leaf ? leaf_d : (outside ? kOutsideDomain : dist));
-        sem = new_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
-        const bool has_sem = sem != 0, near = dist < P.hit_eps;
-        const bool hit = !is_fault && has_sem && near;
+        // the step's distance: the void's exit, the leaf's, the outside-domain
+        // step, or NaN after a fault (so t becomes NaN); a ray's semantic is its
+        // leaf's when the step hits and 0 whenever it ends otherwise, so only
+        // the step that ends a ray needs it (void, outside and fault steps never
+        // hit: their semantic is 0)
+        // (inverse ballots are convergent: read them outside the conditional
+        // expression, which then stays a chain of selects)
+        const bool on_leaf = lane_in(m_leaf), outside = lane_in(~m_dom);
+        const float dist =
+            slot == kSlotVoid ? void_d : (on_leaf ? leaf_d : (outside ? kOutsideDomain : __builtin_nanf("")));
+        const uint64_t m_hit = m_leaf & wave_mask(leaf_s != 0) & wave_mask(dist < P.hit_eps);
         const float t_next = t + dist;
-        const bool far = t_next > P.max_distance, spent = step >= P.max_steps;
-        bool finish = has_ray && (is_fault || hit || far || spent);
-        t = (has_ray && !hit) ? t_next : t;
-        t = (finish && is_fault) ? __builtin_nanf("") : t;
-        sem = (finish && !hit) ? 0 : sem;
-        const bool live = has_ray && !finish;
+        uint64_t m_fin = m_ray & (wave_mask(slot == kSlotFault) | m_hit | wave_mask(t_next > P.max_distance) |
+                                  wave_mask(step >= P.max_steps));
+        t = lane_in(m_ray & ~m_hit) ? t_next : t;
 
         // ---- one more step if the leaf cache answers it alone ----
         // (within the leaf box neither the void cache nor the domain test can
         // fire for tame boxes; it repeats the leaf's distance, so it cannot hit)
-        bool run = live && is_leaf;
+        uint64_t m_run = m_ray & ~m_fin & m_leaf;
 #pragma unroll
         for (uint32_t k = 0; k < kLeafRunFast; ++k) {
             const float ux = __builtin_fmaf(t, fabsf(dx), ox);
             const float uy = __builtin_fmaf(t, fabsf(dy), oy);
             const float uz = __builtin_fmaf(t, fabsf(dz), oz);
-            const bool in_lf2 = ux <= lfx && uy <= lfy && uz <= lfz;
-            run = run && in_lf2;
-            step += run ? 1 : 0;
-            t = run ? t + dist : t;
-            const bool far2 = t > P.max_distance, spent2 = step >= P.max_steps;
-            const bool fin2 = run && (far2 || spent2);
-            sem = fin2 ? 0 : sem;
-            finish = finish || fin2;
-            run = run && !fin2;
+            m_run &= wave_mask(ux <= lfx) & wave_mask(uy <= lfy) & wave_mask(uz <= lfz);
+            step = add_lane_bit(step, m_run);
+            t = lane_in(m_run) ? t + dist : t;
+            const uint64_t m_fin2 = m_run & (wave_mask(t > P.max_distance) | wave_mask(step >= P.max_steps));
+            m_fin |= m_fin2;
+            m_run &= ~m_fin2;
         }
-        has_ray = has_ray && !finish;
-        need |= wave_mask(finish);
-        if (finish) {
+        need |= m_fin;
+        if (lane_in(m_fin)) {
+            const int32_t sem = lane_in(m_hit) ? leaf_s : 0;
             if ((tag >> 31) != 0u) {
                 uint32_t* e = my_stage + ((tag >> 6) & 3u) * kStageWords + (tag & 63u);
                 e[0] = __float_as_uint(t);
