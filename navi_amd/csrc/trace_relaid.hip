@@ -152,6 +152,13 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
     return __builtin_fmaf(e, r, q0);
 }
 
+// LDS addresses as 32-bit byte offsets (the local address space) and back
+typedef __attribute__((address_space(3))) uint32_t lds_u32;
+__device__ __forceinline__ uint32_t lds_address(uint32_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<size_t>((lds_u32*)p));
+}
+__device__ __forceinline__ lds_u32* lds_pointer(uint32_t addr) { return (lds_u32*)static_cast<size_t>(addr); }
+
 // v with its sign flipped where d's sign bit is set (exact): a coordinate in
 // the frame mirrored along each axis on which the ray moves towards -inf
 __device__ __forceinline__ float mirror(float v, float d) {
@@ -444,12 +451,14 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     float lfx = __builtin_nanf(""), lfy = lfx, lfz = lfx, dmx = lfx, dmy = lfx, dmz = lfx;
 
     // ---- output staging: the wave's slots (kStageSlots tiles), their tiles
-    // (uniform), and per lane its ray's slot and position (bit 31 set) or 0
-    // (the ray stores its own outputs) ----
+    // (uniform), and per lane the LDS byte address of its ray's distance in its
+    // tile's slot, or 0 (the ray stores its own outputs; the staging area lies
+    // above the scene table, never at address 0) ----
     const bool stage = P.stage != 0u;
     uint32_t tag = 0, ring = 0;
     uint32_t st0 = kNoTile, st1 = kNoTile, st2 = kNoTile, st3 = kNoTile;
     uint32_t* const my_stage = lds_stage + (threadIdx.x >> 6) * (kStageSlots * kStageWords);
+    const uint32_t stage_addr = lds_address(my_stage);
     const uint32_t flush_pos = P.tile_el ? (((lane & 7u) << 3) | (lane >> 3)) : lane;
     // writes out slot k (tile `tile`) and empties it; every lane of the wave
     // takes one position, eight lanes per run of eight consecutive rays
@@ -547,7 +556,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                         const uint32_t old = k == 0 ? st0 : (k == 1 ? st1 : (k == 2 ? st2 : st3));
                         if (old != kNoTile) {
                             flush_slot(k, old);
-                            const bool evicted = (tag >> 31) != 0u && ((tag >> 6) & 3u) == k;
+                            const bool evicted = tag - (stage_addr + k * kStageWords * 4u) < kStageWords * 4u;
                             tag = evicted ? 0u : tag;
                         }
                         st0 = k == 0 ? T : st0;
@@ -556,7 +565,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                         st3 = k == 3 ? T : st3;
                     }
                     const bool same = fresh && qtile == T;
-                    tag = same ? (0x80000000u | (k << 6) | (q & 63u)) : tag;
+                    tag = same ? stage_addr + k * kStageWords * 4u + (q & 63u) * 4u : tag;
                     todo &= ~wave_mask(same);
                 }
             }
@@ -746,8 +755,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         need |= m_fin;
         if (lane_in(m_fin)) {
             const int32_t sem = lane_in(m_hit) ? leaf_s : 0;
-            if ((tag >> 31) != 0u) {
-                uint32_t* e = my_stage + ((tag >> 6) & 3u) * kStageWords + (tag & 63u);
+            if (tag != 0u) {
+                lds_u32* e = lds_pointer(tag);
                 e[0] = __float_as_uint(t);
                 e[64] = static_cast<uint32_t>(sem);
             } else {
