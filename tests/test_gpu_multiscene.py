@@ -172,6 +172,35 @@ def test_relaid_signed_zero_axes_and_long_ranges(gpu, corpus, max_distance):
              f"zeros/{max_distance}/tiles")
 
 
+def test_relaid_non_finite_and_extreme_rays(gpu, corpus):
+    """Directions with NaN, infinite, huge (beyond 2^126, where a reciprocal
+    leaves the normal range), subnormal, below-1e-4 and signed-zero components,
+    and origins with NaN or infinite coordinates: the record-layout tracer
+    against the oracle (NaN distances compared as NaN)."""
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    rng = np.random.default_rng(77)
+    specials = [np.nan, np.inf, -np.inf, 3e38, -1e38, 1e-40, -1e-42, 5e-5, -9e-5, 0.0, -0.0, 1.0, -1.0]
+    n_env, rays = 4, 256
+    env_scene = (np.arange(n_env) % len(corpus)).astype(np.int32)
+    free = np.stack([corpus[s].free_origins(rng, 1)[0] for s in env_scene]).astype(np.float32)
+    o = np.ascontiguousarray(np.broadcast_to(free[:, None, :], (n_env, rays, 3))).astype(np.float32)
+    d = rng.normal(size=(n_env, rays, 3))
+    d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+    for k in range(rays - 16):
+        axis = k % 3
+        d[:, k, axis] = np.float32(specials[k % len(specials)])
+        if k % 5 == 0:
+            d[:, k, (axis + 1) % 3] = np.float32(specials[(k // 5) % len(specials)])
+    for k in range(rays - 16, rays):  # non-finite origins
+        o[:, k, k % 3] = np.float32([np.nan, np.inf, -np.inf, 1e30][k % 4])
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, o, d, 128, 30.0)
+    _compare(_run(res, env_scene, o, d, 128, 30.0), ref, 30.0, "extreme")
+    _compare(_run(res, env_scene, o, d, 128, 30.0, elevation_bins=16), ref, 30.0, "extreme/tiles")
+
+
 def test_unknown_scene_id_reports_nan(gpu, corpus):
     from navi_amd.multiscene import ResidentScenes
 
