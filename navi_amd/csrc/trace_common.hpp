@@ -97,10 +97,17 @@ __device__ __forceinline__ uint32_t append_bit(uint32_t i, bool b) {
 __device__ __forceinline__ bool lane_in(uint64_t mask) { return __builtin_amdgcn_inverse_ballot_w64(mask); }
 
 // i + (this lane's bit of mask): one add-with-carry, the mask as carry-in.
+// The mask is wave-uniform; reading it through readfirstlane keeps it in
+// scalar registers for the asm operand even where the compiler cannot prove
+// that (free where it can).
 __device__ __forceinline__ int32_t add_lane_bit(int32_t i, uint64_t mask) {
+    // (the builtin returns int: widen through uint32_t, not by sign extension)
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mask >> 32)));
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(mask)));
+    const uint64_t m = (static_cast<uint64_t>(hi) << 32) | lo;
     int32_t r;
     uint64_t carry_out;
-    asm("v_addc_co_u32_e64 %0, %1, %2, 0, %3" : "=v"(r), "=s"(carry_out) : "v"(i), "s"(mask));
+    asm("v_addc_co_u32_e64 %0, %1, %2, 0, %3" : "=v"(r), "=s"(carry_out) : "v"(i), "s"(m));
     return r;
 }
 
