@@ -396,14 +396,14 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
 
 // The fast march: launches whose scenes all have split planes in LDS, tame
 // boxes, no record deeper than 30 levels and no negative leaf distance, with
-// cell tables below 4 GiB (every scene the library's compiler writes). Per ray
-// the results are the general march's; it leaves out what such launches
-// cannot meet: the void cache (it changes nothing in them, see the kernel), the
-// depth counter (the 32-level limit never applies) and the range checks of the
-// exit quotients and of the leaf-run step (tame boxes). Conditions are
-// combined with bitwise operators, so the step's path has no short-circuit
-// branches, and the cell table is read through a buffer resource (32-bit
-// offsets).
+// cell tables below 4 GiB (every scene the library's compiler writes) and a
+// range below the outside-domain distance. Per ray the results are the general
+// march's; it leaves out what such launches cannot meet: the void cache (it
+// changes nothing in them, see the kernel), the depth counter (the 32-level
+// limit never applies), the range checks of the exit quotients and of the
+// leaf-run step (tame boxes) and the box faces behind the ray (below). The
+// step's conditions are wave masks, so its path has no short-circuit branches,
+// and the cell table is read through a buffer resource (32-bit offsets).
 template <int kDepth, int kPD, bool kPoses>
 __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
                                            const float* lds_planes, uint32_t* lds_stage) {
