@@ -151,7 +151,7 @@ def single_scene_config(cfg, dev, threads):
                           "p90": round(float(np.percentile(launches, 90)), 4), "launches": int(launches.size)},
             "rays_per_s": round(E * R / (ms / 1e3), 1),
             "dag_words_per_ray": round(words / (E * R), 3),
-            "roofline": roofline(alg, ms, "trace_relaid_kernel"),
+            "roofline": roofline(alg, ms, "trace_fast_kernel"),
             "cpu_baseline": {"value": round(E * R / t_cpu, 1), "unit": "rays/s", "cores": threads, "kind": "port",
                              "sample": f"the whole ray set ({E * R} rays), median of {CPU_RUNS} runs "
                                        f"after 1 warm-up"},
@@ -244,7 +244,7 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
         "entry_points": ["navi_trace_relaid_poses", "navi_observe"],
         "last_step_moves_kept": round(moved, 4),
         "mean_min_distance": round(float(walk.stats[:, 0].mean().item()), 4),
-        "roofline": roofline(alg, ms, "trace_relaid_kernel + observation_kernel (whole step)"),
+        "roofline": roofline(alg, ms, "trace_fast_kernel + observation_kernel (whole step)"),
         "observation_kernel_roofline": roofline(obs_alg, observe_ms, "observation_kernel"),
         "cpu_baseline": {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
                          "kind": "port",
@@ -330,7 +330,7 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run one device copy of this many MiB (known HBM bytes) so a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run can scale the tracer's counters")
-    ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "trace_relaid_kernel_traffic.json"),
+    ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "trace_fast_kernel_traffic.json"),
                     help="measured HBM bytes per launch (written from rocprofv3 --pmc runs)")
     args = ap.parse_args()
 
@@ -491,7 +491,7 @@ def main() -> int:
             "mean_steps_per_ray": round(mean_steps, 3), "hit_rate": round(hit_rate, 4),
             "dag_words_per_ray": round(total_words / n_rays, 3),
         },
-        "roofline": roofline(alg_bytes, ms, "trace_relaid_kernel", traffic),
+        "roofline": roofline(alg_bytes, ms, "trace_fast_kernel", traffic),
         "cpu_baseline": cpu,
         "parity": par,
         "small_configs": small,

@@ -191,11 +191,11 @@ int navi_trace_relaid(const uint32_t* records, uint64_t n_records, const navi_re
  * counterpart in the reference. Same arguments and results as
  * navi_trace_relaid; it calls no hipMalloc, hipFree or allocating routine at
  * any time, not even on its first call on a device. Its work-queue counter
- * pair lives in a static device array of 256 bytes (each GPU the library runs
+ * words live in a static device array of 256 bytes (each GPU the library runs
  * on holds its copy until the process ends), cleared by a small kernel on
- * `stream` before every launch; a launch needs one pair whatever its size, so
+ * `stream` before every launch; a launch needs three words whatever its size, so
  * the limits are navi_trace_relaid's (at most 2^30 rays, fewer than 2^27
- * records). Every call on one GPU shares that pair: calls that overlap on one
+ * records). Every call on one GPU shares those words: calls that overlap on one
  * GPU (concurrent streams, or graph replays running at once) race and may
  * leave rays unwritten; serialise them, or use navi_trace_relaid.
  */

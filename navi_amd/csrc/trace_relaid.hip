@@ -4,13 +4,18 @@
 // checkout); tests compare both against the CPU oracle bit for bit.
 //
 // Execution model (CDNA4, wave64):
+//   * two kernels: the fast march (monotone, tame, shallow scenes with split
+//     planes, the library compiler's) alone in trace_fast_kernel at eight
+//     waves per SIMD, everything in trace_relaid_kernel at seven; a launch
+//     enqueues the first when its planes fit, the second after it (returning
+//     at once when the first traced the launch), see launch_relaid;
 //   * persistent waves: the grid holds as many workgroups as the chip keeps
 //     resident; waves claim work units (128 rays = two 8 x 8 tiles, or one
 //     tile for batches too small to fill the chip) from a counter pair of
 //     the launch's stream (or of the graph node it was captured into), the
 //     last wave rearming it; without a counter (all 4096 pairs in use) wave
 //     w takes 64-ray chunks w, w + W, ...;
-//   * lane refill: once 8 of 64 lanes have finished their rays, the idle lanes
+//   * lane refill: once 8 (fast march: 12) of 64 lanes have finished their rays, the idle lanes
 //     take the next rays (ballot + mbcnt rank), so a wave never idles on a few
 //     long rays;
 //   * one march step per outer iteration for every lane: the void / domain /
@@ -125,6 +130,7 @@ struct RelaidParams {
     uint32_t unit_rays;            // 128 (2 tiles), or 64 for batches too small to fill the chip
     uint32_t small_tables;         // the cell tables span fewer than 2^32 bytes
     uint32_t stage;                // finished rays staged per tile in LDS (fast march)
+    uint32_t after_fast;           // launched after trace_fast_kernel: return if that one ran
 };
 
 // Work index q -> ray id (env * R + r).
@@ -182,15 +188,15 @@ constexpr uint32_t kRefillMinFast = 12;
 // held by one wave when the queue runs dry, smaller ones cost more claims
 constexpr uint32_t kUnitRays = 128;
 constexpr uint32_t kSmallUnitRays = 64;  // one tile, for small batches
-// Output staging of the fast march: each wave keeps a ring of kStageSlots
-// tiles (64 rays) in LDS, a finished ray's distance and semantic go to its
-// tile's slot, and a slot is written out when a new tile evicts it (or the
-// wave ends): eight consecutive lanes then store eight consecutive rays, whole
-// 32-byte sectors, where a finished ray's own store writes 4 bytes of a line
-// that L2 has long evicted before the rest of its tile is done. A slot
+// Output staging of the fast march: each wave keeps two tiles (64 rays) in
+// LDS slots, a finished ray's distance and semantic go to its tile's slot, and
+// a slot is written out when a new tile takes it over (the slots alternate) or
+// the wave ends: eight consecutive lanes then store eight consecutive rays,
+// whole 32-byte sectors, where a finished ray's own store writes 4 bytes of a
+// line that L2 has long evicted before the rest of its tile is done. A slot
 // position whose semantic is kStageEmpty holds no result (semantics are
 // 15-bit leaf values or 0).
-constexpr uint32_t kStageSlots = 4;
+constexpr uint32_t kStageSlots = 2;
 constexpr uint32_t kStageWords = 128;  // per slot: 64 distances, then 64 semantics
 constexpr uint32_t kStageEmpty = 0xffffffffu;
 constexpr uint32_t kNoTile = 0xffffffffu;
@@ -217,6 +223,8 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 // and planes at 4 waves lose to none.
 constexpr size_t kPlaneLds = 22528;
 constexpr size_t kPlaneLdsWide = 32512;
+// The fast kernel's LDS per workgroup: eight 256-thread workgroups per CU.
+constexpr size_t kFastLds = 20480;
 __host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
 constexpr uint32_t kPlaneHeader = 8;  // floats before the planes: scales, pad, offsets, pad
 __host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) {
@@ -456,7 +464,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     // above the scene table, never at address 0) ----
     const bool stage = P.stage != 0u;
     uint32_t tag = 0, ring = 0;
-    uint32_t st0 = kNoTile, st1 = kNoTile, st2 = kNoTile, st3 = kNoTile;
+    uint32_t st0 = kNoTile, st1 = kNoTile;
     uint32_t* const my_stage = lds_stage + (threadIdx.x >> 6) * (kStageSlots * kStageWords);
     const uint32_t stage_addr = lds_address(my_stage);
     const uint32_t flush_pos = P.tile_el ? (((lane & 7u) << 3) | (lane >> 3)) : lane;
@@ -546,14 +554,10 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                         k = 0;
                     } else if (st1 == T) {
                         k = 1;
-                    } else if (st2 == T) {
-                        k = 2;
-                    } else if (st3 == T) {
-                        k = 3;
                     } else {
                         k = ring;
-                        ring = (ring + 1u) & (kStageSlots - 1u);
-                        const uint32_t old = k == 0 ? st0 : (k == 1 ? st1 : (k == 2 ? st2 : st3));
+                        ring ^= 1u;
+                        const uint32_t old = k == 0 ? st0 : st1;
                         if (old != kNoTile) {
                             flush_slot(k, old);
                             const bool evicted = tag - (stage_addr + k * kStageWords * 4u) < kStageWords * 4u;
@@ -561,8 +565,6 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                         }
                         st0 = k == 0 ? T : st0;
                         st1 = k == 1 ? T : st1;
-                        st2 = k == 2 ? T : st2;
-                        st3 = k == 3 ? T : st3;
                     }
                     const bool same = fresh && qtile == T;
                     tag = same ? stage_addr + k * kStageWords * 4u + (q & 63u) * 4u : tag;
@@ -770,8 +772,6 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     if (stage) {
         if (st0 != kNoTile) flush_slot(0, st0);
         if (st1 != kNoTile) flush_slot(1, st1);
-        if (st2 != kNoTile) flush_slot(2, st2);
-        if (st3 != kNoTile) flush_slot(3, st3);
     }
 }
 
@@ -1217,13 +1217,17 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
     }
 }
 
-template <int kDepth, int kPD, bool kPoses>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
+// A workgroup's set-up: the scene table (and with kPD > 0 the split planes of
+// kPD levels) staged in LDS, and the launch-wide conditions, the same in every
+// workgroup.
+struct LaunchConds {
+    int tame, shallow, planes;
+    bool void_cache;
+};
+
+template <int kPD>
+__device__ LaunchConds stage_scenes(const RelaidParams& P, SceneLds* lds_scenes, float* lds_planes) {
     constexpr bool kPlanes = kPD > 0;
-    static_assert(!kPlanes || (kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7),
-                  "planes of 4..6 levels, the table at most two levels below them");
-    extern __shared__ SceneLds lds_scenes[];
-    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
     // `tame`: every scene box has coordinates below 2^100 in magnitude, so
     // lo + hi never overflows, every split plane lies within its box, each
     // descent box lies within its parent and the domain, and exit quotients
@@ -1242,8 +1246,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         shallow &= d.max_depth <= static_cast<uint32_t>(kMaxDepth - 2) ? 1 : 0;
         monotone &= (d.flags & NAVI_SCENE_NONNEG_LEAVES) ? 1 : 0;
     }
-    tame = __syncthreads_and(tame);
-    shallow = __syncthreads_and(shallow);
+    LaunchConds c;
+    c.tame = __syncthreads_and(tame);
+    c.shallow = __syncthreads_and(shallow);
     // The void cache (kernel.cu:265-267) changes nothing in tame, monotone
     // launches: a point strictly inside the cached void cell lies in the
     // closed box of no other terminal cell (tame boxes nest), so the leaf
@@ -1253,14 +1258,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     // prefix cache then holds that cell's depth-4 ancestor (when it is deeper
     // than 4; else the query stops above depth 4 and saves nothing) and the
     // query leaves every cache as it was. Such launches skip the void cache.
-    const bool void_cache = !(tame && __syncthreads_and(monotone));
+    c.void_cache = !(c.tame && __syncthreads_and(monotone));
     // `planes`: every scene's depth-D cells can be located from its planes
     int planes = kPlanes ? 1 : 0;
-    const uint32_t D = kPlanes ? static_cast<uint32_t>(kDepth) : P.cell_depth;  // the table depth
-    constexpr uint32_t kAxis = kPlanes ? axis_stride(kPD) : 0u;    // floats per axis
-    constexpr uint32_t kScene = kPlanes ? scene_stride(kPD) : 0u;  // floats per scene
-    constexpr uint32_t kCells = kPlanes ? (1u << kPD) : 0u;        // cells per axis
-    if (kPlanes) {
+    if constexpr (kPlanes) {
+        constexpr uint32_t kAxis = axis_stride(kPD);    // floats per axis
+        constexpr uint32_t kScene = scene_stride(kPD);  // floats per scene
+        constexpr uint32_t kCells = 1u << kPD;          // cells per axis
         for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
             const navi_relaid_scene& d = P.scenes[i / 3];
             const int a = i % 3;
@@ -1274,19 +1278,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
         }
         planes = __syncthreads_and(planes);
     }
-    if constexpr (kPlanes) {
-        if (planes && tame && shallow && !void_cache && P.small_tables && P.max_distance < kOutsideDomain)
-            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
-                                            reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * kScene));
-        else
-            march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
-    } else {
-        march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, tame, shallow, planes, void_cache);
-    }
+    c.planes = planes;
+    return c;
+}
+
+// Whether a launch takes the fast march (every workgroup reaches the same answer).
+__device__ __forceinline__ bool fast_applies(const RelaidParams& P, const LaunchConds& c) {
+    return c.planes && c.tame && c.shallow && !c.void_cache && P.small_tables && P.max_distance < kOutsideDomain;
+}
+
+// The last wave to finish rearms the queue for the next launch on this
+// stream: every other wave has made its final claim before counting itself.
+__device__ __forceinline__ void rearm_queue(const RelaidParams& P) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n_waves = (gridDim.x * blockDim.x) >> 6;
-    // The last wave to finish rearms the queue for the next launch on this
-    // stream: every other wave has made its final claim before counting itself.
     if (P.queue != nullptr && lane == 0) {
         if (atomicAdd(P.queue + 1, 1u) == n_waves - 1u) {
             atomicExch(P.queue, 0u);
@@ -1295,14 +1300,62 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     }
 }
 
+// The fast march in a kernel of its own, at eight waves per SIMD (64 vector
+// registers; the general march needs 72, and six waves instead of seven cost
+// the fast march 8% where eight gain it 5%). Launched first when its LDS fits
+// eight workgroups per CU and the launch has a work queue; it records in the
+// queue's third word whether the fast march applied and returns at once when
+// it does not (the general kernel, launched next, then traces the launch).
+template <int kDepth, int kPD, bool kPoses>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void trace_fast_kernel(RelaidParams P) {
+    static_assert(kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7,
+                  "planes of 4..6 levels, the table at most two levels below them");
+    extern __shared__ SceneLds lds_scenes[];
+    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
+    const LaunchConds c = stage_scenes<kPD>(P, lds_scenes, lds_planes);
+    const bool fast = fast_applies(P, c);
+    if (blockIdx.x == 0 && threadIdx.x == 0) P.queue[2] = fast ? 1u : 0u;
+    if (!fast) return;
+    march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
+                                    reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
+    rearm_queue(P);
+}
+
+// Both marches, at seven waves per SIMD: the fast march where it applies (for
+// launches whose LDS does not fit the fast kernel's eight workgroups), else
+// the general one. Launched after trace_fast_kernel (after_fast), it returns at
+// once when that one traced the launch.
+template <int kDepth, int kPD, bool kPoses>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void trace_relaid_kernel(RelaidParams P) {
+    constexpr bool kPlanes = kPD > 0;
+    static_assert(!kPlanes || (kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7),
+                  "planes of 4..6 levels, the table at most two levels below them");
+    if (P.after_fast && __hip_atomic_load(P.queue + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return;
+    extern __shared__ SceneLds lds_scenes[];
+    float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
+    const LaunchConds c = stage_scenes<kPD>(P, lds_scenes, lds_planes);
+    if constexpr (kPlanes) {
+        if (fast_applies(P, c))
+            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
+                                            reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
+        else
+            march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, c.tame, c.shallow, c.planes, c.void_cache);
+    } else {
+        march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, c.tame, c.shallow, c.planes, c.void_cache);
+    }
+    rearm_queue(P);
+}
+
 // Resident waves the chip holds for this kernel: the persistent grid is sized
 // to exactly that, so no wave waits for a slot and the sweep has no second,
 // partly empty round.
 // (per device, kernel variant and LDS size of the launch; guarded by g_queue_mu).
 std::map<std::pair<std::pair<int, int>, size_t>, int> g_grid_blocks;
 
-// Work-queue counters: pairs [next unit, finished waves] in one 32 KiB device
-// buffer per device, allocated and zeroed by navi_device_init. An eager launch
+// Work-queue counters: [next unit, finished waves, the fast kernel traced the
+// launch, unused] in one 64 KiB device buffer per device, allocated and zeroed
+// by navi_device_init (the third word is written by each fast kernel before the
+// general kernel after it reads it; "pair" below means these four words). An eager launch
 // uses the pair of its (stream, thread for hipStreamPerThread): launches on one
 // stream run in order, so the pair is never used by two launches at once, and
 // the kernel's last wave rearms it for the next. A launch recorded into a graph
@@ -1312,6 +1365,7 @@ std::map<std::pair<std::pair<int, int>, size_t>, int> g_grid_blocks;
 // static schedule) once kQueueSlots are in use, or while a stream captures on a
 // device that was never initialised (no allocation inside a capture).
 constexpr int kQueueSlots = 4096;
+constexpr int kQueueWords = 4;
 std::mutex g_queue_mu;
 struct DeviceQueues {
     uint32_t* mem = nullptr;
@@ -1325,9 +1379,9 @@ int init_device_locked(int dev) {
     DeviceQueues& q = g_queues[dev];
     if (q.mem != nullptr) return NAVI_OK;
     void* p = nullptr;
-    if (hipMalloc(&p, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess)
+    if (hipMalloc(&p, kQueueSlots * kQueueWords * sizeof(uint32_t)) != hipSuccess)
         return set_error(NAVI_E_NOMEM, "work-queue counters: hipMalloc failed on device %d", dev);
-    if (hipMemset(p, 0, kQueueSlots * 2 * sizeof(uint32_t)) != hipSuccess ||
+    if (hipMemset(p, 0, kQueueSlots * kQueueWords * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         (void)hipFree(p);
         return set_error(NAVI_E_LAUNCH, "work-queue counters: clearing failed on device %d", dev);
@@ -1345,7 +1399,7 @@ uint32_t* queue_for(hipStream_t stream) {
     std::lock_guard<std::mutex> lock(g_queue_mu);
     DeviceQueues& q = g_queues[dev];
     if (q.mem == nullptr && (capturing || init_device_locked(dev) != NAVI_OK)) return nullptr;
-    if (capturing) return q.used < kQueueSlots ? q.mem + 2 * q.used++ : nullptr;
+    if (capturing) return q.used < kQueueSlots ? q.mem + kQueueWords * q.used++ : nullptr;
     const size_t thread = stream == hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
     const auto key = std::make_pair(static_cast<void*>(stream), thread);
     auto it = q.slot.find(key);
@@ -1353,15 +1407,15 @@ uint32_t* queue_for(hipStream_t stream) {
         if (q.used >= kQueueSlots) return nullptr;
         it = q.slot.emplace(key, q.used++).first;
     }
-    return q.mem + 2 * it->second;
+    return q.mem + kQueueWords * it->second;
 }
 
-// Scratch of navi_trace_relaid_noalloc: one work-queue counter pair per device
+// Scratch of navi_trace_relaid_noalloc: one set of work-queue counter words per device
 // in a static device array (each GPU the library runs on holds its own copy
 // until the process ends). Host code never uses the array's name as an
 // address: navi_device_init (or the entry point's first call on a device)
 // looks up the device's copy with hipGetSymbolAddress and keeps the pointer.
-constexpr int kScratchWords = 64;  // 256 bytes; a launch uses words 0 and 1
+constexpr int kScratchWords = 64;  // 256 bytes; a launch uses words 0 to 2
 constexpr int kMaxDevices = 64;
 uint32_t* g_scratch_ptr[kMaxDevices] = {};  // guarded by g_queue_mu
 
@@ -1387,41 +1441,117 @@ int scratch_locked(int dev, uint32_t** out) {
     return NAVI_OK;
 }
 
-// Zeroes the counter pair before a launch that shares it (a kernel node, never a
+// Zeroes the counter words before a launch that shares them (a kernel node, never a
 // memset node, so the launch can be captured into a graph).
 __global__ void clear_queue_kernel(uint32_t* queue) {
-    if (threadIdx.x < 2) queue[threadIdx.x] = 0u;
+    if (threadIdx.x < 3) queue[threadIdx.x] = 0u;
 }
 
-// queue: the counter pair to use (no_alloc), or null to take the stream's pair.
+// Grid blocks of a persistent launch of `kernel` with `lds` bytes per workgroup:
+// the workgroups the chip holds at once (cached per device, variant and LDS).
+int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool keep) {
+    constexpr int kThreads = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    const auto key = std::make_pair(std::make_pair(dev, variant), lds);
+    {
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        auto it = g_grid_blocks.find(key);
+        if (it != g_grid_blocks.end()) return it->second;
+    }
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 4;
+    const int blocks = cus * per_cu;
+    if (keep) {  // the no-allocation entry point keeps no host table entry either
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        g_grid_blocks[key] = blocks;
+    }
+    return blocks;
+}
+
+// Sizes the work units and the grid of one persistent launch and enqueues it.
+int enqueue_relaid(void (*kernel)(RelaidParams), RelaidParams P, int variant, size_t lds, bool keep,
+                   hipStream_t stream) {
+    constexpr int kThreads = 256;
+    const int grid_blocks = resident_blocks(kernel, variant, lds, keep);
+    // Small batches: one-tile units, so that more waves get work (a launch
+    // wants several units per resident wave to balance the long rays).
+    P.unit_rays = kUnitRays;
+    if (static_cast<int64_t>(P.n_rays) < static_cast<int64_t>(kUnitRays) * 4 * 4 * grid_blocks)
+        P.unit_rays = kSmallUnitRays;
+    P.n_units = (P.n_rays + P.unit_rays - 1u) / P.unit_rays;
+    int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
+    if (blocks > grid_blocks) blocks = grid_blocks;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+    return NAVI_OK;
+}
+
+// The deepest split-plane depth P <= min(D, 6), at most two levels above the
+// table, whose planes and scene table fit `budget` bytes; 0 if none does.
+int plane_depth_for(int32_t n_scenes, uint32_t D, size_t budget) {
+    for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p)
+        if (static_cast<size_t>(n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) return p;
+    return 0;
+}
+
+// queue: the counter words to use (no_alloc), or null to take the stream's.
+// A launch whose planes fit kFastLds (and that has a queue, a range below the
+// outside-domain distance and small tables) enqueues trace_fast_kernel, then
+// trace_relaid_kernel with after_fast, which returns at once when the fast
+// kernel traced it (every other launch: trace_relaid_kernel alone).
 int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = nullptr) {
     const bool no_alloc = scratch_queue != nullptr;
     P.n_chunks = (P.n_rays + 63u) / 64u;
-    P.unit_rays = kUnitRays;
     P.queue = no_alloc ? scratch_queue : queue_for(stream);
-    constexpr int kThreads = 256;
-    // Split planes of the deepest P <= min(D, 6), at most two levels above the
-    // table, whose LDS (with the scene table) fits kPlaneLds, else kPlaneLdsWide;
-    // none if no P does.
     const uint32_t D = P.cell_depth;
     P.small_tables = (static_cast<uint64_t>(P.n_scenes) << (3u * D + 3u)) < (1ull << 32) ? 1u : 0u;
-    int pd = 0;
-    for (const size_t budget : {kPlaneLds, kPlaneLdsWide}) {
-        for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p) {
-            if (static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) {
-                pd = p;
-                break;
-            }
+    const bool poses = P.local_dirs != nullptr;
+    if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
+
+    // the fast kernel: planes that fit eight workgroups per CU
+    const int pf = plane_depth_for(P.n_scenes, D, kFastLds);
+    P.after_fast = 0u;
+    if (pf != 0 && P.queue != nullptr && P.small_tables && P.max_distance < kOutsideDomain) {
+        RelaidParams F = P;
+        size_t lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pf) * sizeof(float));
+        F.stage = (F.out_steps == nullptr && lds + kStageLds <= kFastLds) ? 1u : 0u;
+        if (F.stage) lds += kStageLds;
+        void (*fast)(RelaidParams) = nullptr;
+#define NAVI_FAST(d, p) (poses ? trace_fast_kernel<d, p, true> : trace_fast_kernel<d, p, false>)
+        switch (pf * 8 + static_cast<int>(D)) {
+            case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
+            case 4 * 8 + 5: fast = NAVI_FAST(5, 4); break;
+            case 4 * 8 + 6: fast = NAVI_FAST(6, 4); break;
+            case 5 * 8 + 5: fast = NAVI_FAST(5, 5); break;
+            case 5 * 8 + 6: fast = NAVI_FAST(6, 5); break;
+            case 5 * 8 + 7: fast = NAVI_FAST(7, 5); break;
+            case 6 * 8 + 6: fast = NAVI_FAST(6, 6); break;
+            case 6 * 8 + 7: fast = NAVI_FAST(7, 6); break;
+            default: break;
         }
-        if (pd) break;
+#undef NAVI_FAST
+        if (fast != nullptr) {
+            const int variant = 2 * (pf * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 1024;
+            const int code = enqueue_relaid(fast, F, variant, lds, !no_alloc, stream);
+            if (code != NAVI_OK) return code;
+            P.after_fast = 1u;
+        }
     }
+
+    // both marches at seven waves: planes fitting kPlaneLds, else kPlaneLdsWide
+    int pd = plane_depth_for(P.n_scenes, D, kPlaneLds);
+    if (pd == 0) pd = plane_depth_for(P.n_scenes, D, kPlaneLdsWide);
     size_t lds = static_cast<size_t>(P.n_scenes) * (sizeof(SceneLds) + (pd ? scene_stride(pd) * sizeof(float) : 0));
     // output staging where it fits the budget the planes were sized for (and
     // no step counts are asked for: those are stored per ray)
     P.stage = (pd != 0 && P.out_steps == nullptr && lds + kStageLds <= (lds <= kPlaneLds ? kPlaneLds : kPlaneLdsWide))
                   ? 1u : 0u;
     if (P.stage) lds += kStageLds;
-    const bool poses = P.local_dirs != nullptr;
     void (*kernel)(RelaidParams) = nullptr;
 #define NAVI_RELAID(d, p) (poses ? trace_relaid_kernel<d, p, true> : trace_relaid_kernel<d, p, false>)
     switch (pd * 8 + static_cast<int>(D)) {
@@ -1436,40 +1566,8 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
         default: kernel = NAVI_RELAID(0, 0); break;
     }
 #undef NAVI_RELAID
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    const auto key = std::make_pair(std::make_pair(dev, 2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses)), lds);
-    int grid_blocks = 0;
-    {
-        std::lock_guard<std::mutex> lock(g_queue_mu);
-        auto it = g_grid_blocks.find(key);
-        if (it != g_grid_blocks.end()) grid_blocks = it->second;
-    }
-    if (grid_blocks == 0) {
-        int cus = 0, per_cu = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
-            per_cu = 4;
-        grid_blocks = cus * per_cu;
-        if (!no_alloc) {  // the no-allocation entry point keeps no host table entry either
-            std::lock_guard<std::mutex> lock(g_queue_mu);
-            g_grid_blocks[key] = grid_blocks;
-        }
-    }
-    // Small batches: one-tile units, so that more waves get work (a launch
-    // wants several units per resident wave to balance the long rays).
-    if (static_cast<int64_t>(P.n_rays) < static_cast<int64_t>(kUnitRays) * 4 * 4 * grid_blocks)
-        P.unit_rays = kSmallUnitRays;
-    P.n_units = (P.n_rays + P.unit_rays - 1u) / P.unit_rays;
-    int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
-    if (blocks > grid_blocks) blocks = grid_blocks;
-    if (blocks < 1) blocks = 1;
-    if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
-    return NAVI_OK;
+    return enqueue_relaid(kernel, P, 2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses), lds, !no_alloc,
+                          stream);
 }
 
 }  // namespace navi

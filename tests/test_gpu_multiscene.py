@@ -201,6 +201,53 @@ def test_relaid_non_finite_and_extreme_rays(gpu, corpus):
     _compare(_run(res, env_scene, o, d, 128, 30.0, elevation_bins=16), ref, 30.0, "extreme/tiles")
 
 
+def test_relaid_fast_and_general_launches_interleaved(gpu, corpus):
+    """Launches on one stream alternate between scene sets the fast kernel traces
+    (monotone) and ones it hands to the general kernel (a scene with negative
+    leaf distances), with and without step counts and at both sides of the
+    outside-domain range: every launch against the oracle, so a fast kernel's
+    record of whether it traced the launch is read by its own launch's general
+    kernel only."""
+    from navi_amd.multiscene import ResidentScenes
+
+    mono = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus[:2]])
+    bits = np.array([0x3C00, 0xBC00, 0x2E66, 0xAE66, 0x3800], np.uint32)  # 1, -1, 0.1, -0.1, 0.5
+    words, _ = _full_octree_words(3, bits)
+    neg = ResidentScenes([(words, [-1.0, -1.0, -1.0], [1.0, 1.0, 1.0])])
+    from navi_amd import _native
+
+    flags = neg.relaid_table.cpu().numpy().view(np.uint32)[11]
+    assert not flags & _native.SCENE_NONNEG_LEAVES  # not monotone: the general march
+    rng = np.random.default_rng(5)
+    env_m, o_m, d_m = _rays(corpus[:2], 6, 32, 16, seed=12)
+    o_n = rng.uniform(-1.2, 1.2, (3, 512, 3)).astype(np.float32)
+    d_n = rng.normal(size=(3, 512, 3))
+    d_n = (d_n / np.linalg.norm(d_n, axis=-1, keepdims=True)).astype(np.float32)
+    env_n = np.zeros(3, np.int32)
+    ref_m = _oracle_multi([c.words for c in corpus[:2]], [c.bbox_min_list + c.bbox_max for c in corpus[:2]],
+                          env_m, o_m, d_m, 128, 30.0)
+    ref_n = _oracle_multi([words], [[-1.0, -1.0, -1.0, 1.0, 1.0, 1.0]], env_n, o_n, d_n, 64, 30.0)
+    ref_nl = _oracle_multi([words], [[-1.0, -1.0, -1.0, 1.0, 1.0, 1.0]], env_n, o_n, d_n, 64, 1500.0)
+    import torch
+
+    dev = mono.device
+    t_es = torch.from_numpy(env_m).to(dev)
+    t_o = torch.from_numpy(np.ascontiguousarray(o_m)).to(dev)
+    t_d = torch.from_numpy(np.ascontiguousarray(d_m)).to(dev)
+    out_d = torch.empty(o_m.shape[:2], device=dev)
+    out_s = torch.empty(o_m.shape[:2], device=dev, dtype=torch.int32)
+    for rep in range(3):
+        _compare(_run(mono, env_m, o_m, d_m, 128, 30.0, elevation_bins=16), ref_m, 30.0, f"mono/{rep}")
+        _compare(_run(neg, env_n, o_n, d_n, 64, 30.0), ref_n, 30.0, f"negative/{rep}")
+        # without step counts: the fast kernel stages its outputs
+        mono.cast_rays(t_es, t_o, t_d, out_d, out_s, 128, 30.0, elevation_bins=16)
+        torch.cuda.synchronize()
+        assert np.array_equal(out_d.cpu().numpy().view(np.uint32), ref_m["distance"].view(np.uint32)), f"staged/{rep}"
+        assert np.array_equal(out_s.cpu().numpy(), ref_m["semantic"]), f"staged/{rep}"
+        _compare(_run(neg, env_n, o_n, d_n, 64, 1500.0), ref_nl, 1500.0, f"negative-long/{rep}")
+        _compare(_run(mono, env_m, o_m, d_m, 128, 30.0), ref_m, 30.0, f"mono-linear/{rep}")
+
+
 def test_unknown_scene_id_reports_nan(gpu, corpus):
     from navi_amd.multiscene import ResidentScenes
 
