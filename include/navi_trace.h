@@ -228,6 +228,17 @@ int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const n
                             int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                             void* stream);
 
+/*
+ * Launch shape of the record-layout tracer (no reference counterpart: a tuning
+ * knob of this library). Launches of at least `n_rays` rays whose scenes'
+ * split planes fit two levels below the cell tables in 80 KiB of LDS run in
+ * 1024-thread workgroups (two per CU); smaller launches, whose few workgroups
+ * then spread over more CUs, in 256-thread ones. Results are identical either
+ * way. Process-wide, thread-safe; takes effect from the next launch. Returns
+ * the previous value (default 2^19).
+ */
+uint64_t navi_set_wide_min_rays(uint64_t n_rays);
+
 /* Point-SDF queries (device pointers; see navi_point_query). */
 typedef struct navi_point_queries {
     const uint32_t* records;           /* the record pool of navi_trace_relaid */

@@ -38,6 +38,8 @@ _lib.navi_version.argtypes = []
 
 _lib.navi_device_init.restype = ctypes.c_int
 _lib.navi_device_init.argtypes = []
+_lib.navi_set_wide_min_rays.restype = ctypes.c_uint64
+_lib.navi_set_wide_min_rays.argtypes = [ctypes.c_uint64]
 
 _lib.navi_cast_rays.restype = ctypes.c_int
 _lib.navi_cast_rays.argtypes = [
@@ -165,6 +167,15 @@ SCENE_DESC_DTYPE = [("word_offset", "<u8"), ("n_words", "<u8"), ("bbox_min", "<f
 
 def lib() -> ctypes.CDLL:
     return _lib
+
+
+def set_wide_min_rays(n_rays: int) -> int:
+    """Launches of the record-layout tracer with at least ``n_rays`` rays run in
+    1024-thread workgroups when their split planes fit (results are identical);
+    returns the previous threshold."""
+    if not 0 <= int(n_rays) < (1 << 64):
+        raise ValueError("n_rays must fit an unsigned 64-bit integer")
+    return int(_lib.navi_set_wide_min_rays(int(n_rays)))
 
 
 def version() -> str:

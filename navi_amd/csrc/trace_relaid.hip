@@ -44,6 +44,7 @@
 // multiply-high division by the (uniform) rays-per-env and tile counts.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <cmath>
 #include <map>
 #include <mutex>
@@ -200,7 +201,11 @@ constexpr uint32_t kStageSlots = 2;
 constexpr uint32_t kStageWords = 128;  // per slot: 64 distances, then 64 semantics
 constexpr uint32_t kStageEmpty = 0xffffffffu;
 constexpr uint32_t kNoTile = 0xffffffffu;
-constexpr size_t kStageLds = 4 * kStageSlots * kStageWords * sizeof(uint32_t);  // four waves per workgroup
+// staging bytes of a workgroup of `threads` threads
+__host__ __device__ constexpr size_t stage_lds(int threads) {
+    return static_cast<size_t>(threads / 64) * kStageSlots * kStageWords * sizeof(uint32_t);
+}
+constexpr size_t kStageLds = stage_lds(256);
 
 // A scene as the kernel reads it, staged in LDS once per workgroup so a lane
 // keeps only its scene index in registers.
@@ -225,40 +230,83 @@ constexpr size_t kPlaneLds = 22528;
 constexpr size_t kPlaneLdsWide = 32512;
 // The fast kernel's LDS per workgroup: eight 256-thread workgroups per CU.
 constexpr size_t kFastLds = 20480;
+// The wide fast kernel: two 1024-thread workgroups per CU (eight waves per
+// SIMD), each with half the CU's 160 KiB of LDS, room for split planes two
+// levels below the cell table (the first two levels below the table then take
+// their octants from the plane index: no midpoints, comparisons or selects).
+constexpr int kWideThreads = 1024;
+constexpr size_t kFastLdsWide = 81920;
+// Launches of fewer rays take the 256-thread workgroups: a small batch's few
+// workgroups then spread over more CUs (the wide grid holds as many waves, in
+// a quarter of the workgroups). Measured: 786 K rays on one 512^3 scene 3%
+// faster wide, 49 K rays 8% slower. navi_set_wide_min_rays changes it.
+constexpr uint64_t kWideMinRays = 1u << 19;
+std::atomic<uint64_t> g_wide_min_rays{kWideMinRays};
 __host__ __device__ constexpr uint32_t axis_stride(uint32_t depth) { return (1u << depth) + 2u; }
 constexpr uint32_t kPlaneHeader = 8;  // floats before the planes: scales, pad, offsets, pad
 __host__ __device__ constexpr uint32_t scene_stride(uint32_t depth) {
     return (kPlaneHeader + 3u * axis_stride(depth) + 3u) & ~3u;
 }
 
-// Split planes of one axis for n = 2^D cells (pl[k] = P_k, then the pad), its
-// scale and offset, nested midpoints computed with the descent's own
+// Split planes of every scene and axis for n = 2^P cells (pl[k] = P_k, then
+// a pad float), with the per-axis scale and offset, computed by the whole
+// workgroup: the nested midpoints level by level with the descent's own
 // operations (kernel.cu:165-176), so cell boxes are the descent's boxes bit
-// for bit. Returns whether they support the direct cell lookup of plane_cell:
-// finite, each within 0.2 cell of the uniform grid, an accurate scale, and an
-// offset below 2^14 in magnitude (so it is exact to 2^-10 cell).
-__device__ bool make_planes(float lo, float hi, uint32_t n, float* pl, float& scale_out, float& off_out) {
-    pl[0] = lo;
-    pl[n] = hi;
-    // once per workgroup: kept rolled (unrolled, it would crowd the registers
-    // of the whole kernel)
+// for bit. Returns (to every thread) whether they support the direct cell
+// lookup of plane_cell: finite, each within 0.2 cell of the uniform grid, an
+// accurate scale, and an offset below 2^14 in magnitude (so it is exact to
+// 2^-10 cell).
+template <int kPD>
+__device__ bool stage_planes(const RelaidParams& P, float* lds_planes) {
+    constexpr uint32_t kAxis = axis_stride(kPD);    // floats per axis
+    constexpr uint32_t kScene = scene_stride(kPD);  // floats per scene
+    constexpr uint32_t n = 1u << kPD;               // cells per axis
+    const uint32_t pairs = 3u * static_cast<uint32_t>(P.n_scenes);
+    int ok = 1;
+    for (uint32_t i = threadIdx.x; i < pairs; i += blockDim.x) {
+        const navi_relaid_scene& d = P.scenes[i / 3u];
+        const uint32_t a = i % 3u;
+        float* hdr = lds_planes + (i / 3u) * kScene;
+        float* pl = hdr + kPlaneHeader + a * kAxis;
+        const float lo = d.bbox_min[a], hi = d.bbox_max[a];
+        pl[0] = lo;
+        pl[n] = hi;
+        pl[n + 1] = 0.0f;
+        const float w = hi - lo;
+        const float scale = static_cast<float>(n) / w;
+        const float off = __builtin_fmaf(-lo, scale, -0.25f);
+        const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / n;
+        ok &= (w > 0.0f && w <= 0x1p127f && scale > 0.0f && scale <= 0x1p127f && cw > 0.0 &&
+               fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6 && fabsf(off) <= 0x1p14f) ? 1 : 0;
+        hdr[a] = scale;
+        hdr[4 + a] = off;
+        if (a == 0) hdr[3] = hdr[7] = 0.0f;
+    }
+    __syncthreads();
+    // level by level: the midpoints of step-wide spans, `per` of them per axis
 #pragma unroll 1
-    for (uint32_t step = n; step > 1; step >>= 1)
+    for (uint32_t step = n; step > 1u; step >>= 1) {
+        const uint32_t per = n / step;
 #pragma unroll 1
-        for (uint32_t k = 0; k < n; k += step) pl[k + step / 2] = (pl[k] + pl[k + step]) * 0.5f;
-    const float w = hi - lo;
-    const float scale = static_cast<float>(n) / w;
-    const float off = __builtin_fmaf(-lo, scale, -0.25f);
-    const double cw = (static_cast<double>(hi) - static_cast<double>(lo)) / n;
-    bool ok = w > 0.0f && w <= 0x1p127f && scale > 0.0f && scale <= 0x1p127f && cw > 0.0 &&
-              fabs(static_cast<double>(scale) * cw - 1.0) <= 1e-6 && fabsf(off) <= 0x1p14f;
+        for (uint32_t i = threadIdx.x; i < pairs * per; i += blockDim.x) {
+            const uint32_t pair = i / per;
+            const uint32_t k = (i % per) * step;
+            float* pl = lds_planes + (pair / 3u) * kScene + kPlaneHeader + (pair % 3u) * kAxis;
+            pl[k + step / 2u] = (pl[k] + pl[k + step]) * 0.5f;
+        }
+        __syncthreads();
+    }
 #pragma unroll 1
-    for (uint32_t k = 0; k <= n; ++k)
-        ok = ok && fabs(static_cast<double>(pl[k]) - (static_cast<double>(lo) + k * cw)) <= 0.2 * cw;
-    scale_out = scale;
-    off_out = off;
-    pl[n + 1] = 0.0f;
-    return ok;
+    for (uint32_t i = threadIdx.x; i < pairs * (n + 1u); i += blockDim.x) {
+        const uint32_t pair = i / (n + 1u);
+        const uint32_t k = i % (n + 1u);
+        const navi_relaid_scene& d = P.scenes[pair / 3u];
+        const uint32_t a = pair % 3u;
+        const float* pl = lds_planes + (pair / 3u) * kScene + kPlaneHeader + a * kAxis;
+        const double lo = d.bbox_min[a], cw = (static_cast<double>(d.bbox_max[a]) - lo) / n;
+        ok &= fabs(static_cast<double>(pl[k]) - (lo + k * cw)) <= 0.2 * cw ? 1 : 0;
+    }
+    return __syncthreads_and(ok) != 0;
 }
 
 // Depth-D cell of p along one axis from its planes (pl[k] = P_k, P_0 = lo),
@@ -415,13 +463,24 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
 template <int kDepth, int kPD, bool kPoses>
 __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
                                            const float* lds_planes, uint32_t* lds_stage) {
-    static_assert(kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2, "planes of 4..6 levels");
+    static_assert(kPD >= 4 && kPD <= 8 && kDepth >= 4 && kDepth <= kPD + 2 && kDepth <= 7,
+                  "planes of 4..8 levels, the table at most two levels below them");
     constexpr uint32_t D = kDepth;                    // the table depth
     constexpr uint32_t kAxis = axis_stride(kPD);      // floats per axis
     constexpr uint32_t kScene = scene_stride(kPD);    // floats per scene
     constexpr uint32_t kCells = 1u << kPD;            // cells per axis
     constexpr uint32_t kShP = kPD - kPrefixDepth;     // depth-kPD index >> kShP = depth-4 index
-    constexpr uint32_t kShD = D - kPrefixDepth;       // depth-D index >> kShD = depth-4 index
+    // the cell indices a descent carries are at depth kJ: the table's when it
+    // lies below the planes (splits in registers), else the planes' (the table
+    // index is then the plane index shifted by kUp, and the levels between
+    // the two take their octants from the plane index's bits)
+    constexpr uint32_t kJ = D > kPD ? D : kPD;
+    constexpr uint32_t kUp = kPD - (D < kPD ? D : kPD);
+    constexpr uint32_t kShD = kJ - kPrefixDepth;      // depth-kJ index >> kShD = depth-4 index
+    // the prefix cache's packed fields (a depth-kPD upper-face index is at most 2^kPD)
+    constexpr uint32_t kFW = kPD >= 8 ? 10u : 8u;
+    constexpr uint32_t kFMask = (1u << kFW) - 1u;
+    constexpr uint32_t kOnes = 1u | (1u << kFW) | (1u << (2u * kFW));
     const uint32_t lane = threadIdx.x & 63u;
     // indexed by slot (4 bytes) and by table entry (8 bytes)
     const __amdgpu_buffer_rsrc_t records = __builtin_amdgcn_make_buffer_rsrc(
@@ -610,7 +669,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             uint32_t jz = plane_cell(pz, offs.z, scale.z, plz, kCells, cur.z0, cur.z1);
             // the prefix cache matters only on an upper face of the cached
             // cell (kernel.cu:120-132); see the general march
-            const uint32_t ux = pre_cell & 0xffu, uy = (pre_cell >> 8) & 0xffu, uz = pre_cell >> 16;
+            const uint32_t ux = pre_cell & kFMask, uy = (pre_cell >> kFW) & kFMask, uz = pre_cell >> (2u * kFW);
             const bool ex = jx == ux, ey = jy == uy, ez = jz == uz;
             const bool lx0 = px == cur.x0, ly0 = py == cur.y0, lz0 = pz == cur.z0;
             const bool fx = ex && lx0, fy = ey && ly0, fz = ez && lz0;
@@ -652,10 +711,12 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             }
             // ---- one cell-table read: the slot D levels down, and its depth ----
             const navi_u32x2 e = navi_struct_load_b64(
-                tables, static_cast<int32_t>(my_table | (jz << (2u * D)) | (jy << D) | jx), 0, 0, 0);
+                tables,
+                static_cast<int32_t>(my_table | ((jz >> kUp) << (2u * D)) | ((jy >> kUp) << D) | (jx >> kUp)), 0,
+                0, 0);
             slot = e[0];
-            const uint32_t depth = e[1];
-            if (depth < D) {
+            uint32_t depth = e[1];
+            if (kPD <= D && depth < D) {
                 // a leaf / void / fault above depth D: its box from the planes
                 // down to depth kPD, splits below
                 const uint32_t dp = min(depth, static_cast<uint32_t>(kPD));
@@ -682,16 +743,38 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             // per axis ((j >> kShD) + 1) << kShP, on the three indices packed in
             // 8-bit fields (j < 128: no field carries into the next)
             constexpr uint32_t kLow = (1u << kShD) - 1u;
-            constexpr uint32_t kKeep = (0xffu & ~kLow) * 0x010101u;
-            const uint32_t packed = jx | (jy << 8) | (jz << 16);
-            const uint32_t saved = ((packed & kKeep) >> (kShD - kShP)) + (1u << kShP) * 0x010101u;
+            constexpr uint32_t kKeep = (kFMask & ~kLow) * kOnes;
+            const uint32_t packed = jx | (jy << kFW) | (jz << (2u * kFW));
+            const uint32_t saved = ((packed & kKeep) >> (kShD - kShP)) + (1u << kShP) * kOnes;
             pre_cell = save ? saved : pre_cell;
 
-            // ---- below depth D: one 4-byte slot per level (kernel.cu:136-199) ----
-            // (at most 32 - D trips, see the general march)
+            if constexpr (kPD > D) {
+                // ---- from the table down to depth kPD: the octants are the
+                // plane index's bits (kernel.cu:165-176 picks the same ones:
+                // the depth-kPD cell lies in the box each split leads to) ----
+#pragma unroll
+                for (uint32_t l = D; l < static_cast<uint32_t>(kPD); ++l) {
+                    if (slot < kSlotBadChild) {  // an internal node at depth l
+                        const uint32_t b = kPD - 1u - l;
+                        const uint32_t oct = ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2);
+                        slot = navi_struct_load_b32(records, static_cast<int32_t>((slot << 3) | oct), 0, 0, 0);
+                        depth = l + 1u;
+                    }
+                }
+                if (depth < static_cast<uint32_t>(kPD)) {
+                    // a leaf / void / fault above depth kPD: its box from the planes
+                    const uint32_t up = kPD - depth;
+                    const uint32_t w = 1u << up;
+                    const uint32_t kx = (jx >> up) << up, ky = (jy >> up) << up, kz = (jz >> up) << up;
+                    cur = Box{plx[kx], ply[ky], plz[kz], plx[kx + w], ply[ky + w], plz[kz + w]};
+                }
+            }
+
+            // ---- below depth kJ: one 4-byte slot per level (kernel.cu:136-199) ----
+            // (at most 32 - kJ trips, see the general march)
             uint32_t cur_rec = slot;
             bool deeper = slot < kSlotBadChild;
-            for (uint32_t trip = D; deeper && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
+            for (uint32_t trip = kJ; deeper && trip < static_cast<uint32_t>(kMaxDepth); ++trip) {
                 slot = navi_struct_load_b32(records, static_cast<int32_t>(descend_index(px, py, pz, cur, cur_rec)), 0, 0, 0);
                 cur_rec = slot;
                 deeper = slot < kSlotBadChild;
@@ -1260,24 +1343,8 @@ __device__ LaunchConds stage_scenes(const RelaidParams& P, SceneLds* lds_scenes,
     // query leaves every cache as it was. Such launches skip the void cache.
     c.void_cache = !(c.tame && __syncthreads_and(monotone));
     // `planes`: every scene's depth-D cells can be located from its planes
-    int planes = kPlanes ? 1 : 0;
-    if constexpr (kPlanes) {
-        constexpr uint32_t kAxis = axis_stride(kPD);    // floats per axis
-        constexpr uint32_t kScene = scene_stride(kPD);  // floats per scene
-        constexpr uint32_t kCells = 1u << kPD;          // cells per axis
-        for (int32_t i = threadIdx.x; i < 3 * P.n_scenes; i += blockDim.x) {
-            const navi_relaid_scene& d = P.scenes[i / 3];
-            const int a = i % 3;
-            float* hdr = lds_planes + (i / 3) * kScene;
-            float scale = 0.0f, off = 0.0f;
-            planes &= make_planes(d.bbox_min[a], d.bbox_max[a], kCells, hdr + kPlaneHeader + a * kAxis, scale, off)
-                          ? 1 : 0;
-            hdr[a] = scale;
-            hdr[4 + a] = off;
-            if (a == 0) hdr[3] = hdr[7] = 0.0f;
-        }
-        planes = __syncthreads_and(planes);
-    }
+    int planes = 0;
+    if constexpr (kPlanes) planes = stage_planes<kPD>(P, lds_planes) ? 1 : 0;
     c.planes = planes;
     return c;
 }
@@ -1306,10 +1373,10 @@ __device__ __forceinline__ void rearm_queue(const RelaidParams& P) {
 // eight workgroups per CU and the launch has a work queue; it records in the
 // queue's third word whether the fast march applied and returns at once when
 // it does not (the general kernel, launched next, then traces the launch).
-template <int kDepth, int kPD, bool kPoses>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8))) void trace_fast_kernel(RelaidParams P) {
-    static_assert(kPD >= 4 && kPD <= 6 && kDepth >= kPD && kDepth <= kPD + 2 && kDepth <= 7,
-                  "planes of 4..6 levels, the table at most two levels below them");
+template <int kDepth, int kPD, bool kPoses, int kThreads>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void trace_fast_kernel(RelaidParams P) {
+    static_assert(kPD >= 4 && kPD <= 8 && kDepth >= 4 && kDepth <= kPD + 2 && kDepth <= 7,
+                  "planes of 4..8 levels, the table at most two levels below them");
     extern __shared__ SceneLds lds_scenes[];
     float* const lds_planes = reinterpret_cast<float*>(lds_scenes + P.n_scenes);
     const LaunchConds c = stage_scenes<kPD>(P, lds_scenes, lds_planes);
@@ -1449,8 +1516,7 @@ __global__ void clear_queue_kernel(uint32_t* queue) {
 
 // Grid blocks of a persistent launch of `kernel` with `lds` bytes per workgroup:
 // the workgroups the chip holds at once (cached per device, variant and LDS).
-int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool keep) {
-    constexpr int kThreads = 256;
+int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool keep, int threads) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
     const auto key = std::make_pair(std::make_pair(dev, variant), lds);
@@ -1461,8 +1527,8 @@ int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool 
     }
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess || per_cu <= 0)
-        per_cu = 4;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, lds) != hipSuccess || per_cu <= 0)
+        per_cu = 1;
     const int blocks = cus * per_cu;
     if (keep) {  // the no-allocation entry point keeps no host table entry either
         std::lock_guard<std::mutex> lock(g_queue_mu);
@@ -1473,19 +1539,19 @@ int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool 
 
 // Sizes the work units and the grid of one persistent launch and enqueues it.
 int enqueue_relaid(void (*kernel)(RelaidParams), RelaidParams P, int variant, size_t lds, bool keep,
-                   hipStream_t stream) {
-    constexpr int kThreads = 256;
-    const int grid_blocks = resident_blocks(kernel, variant, lds, keep);
+                   hipStream_t stream, int threads = 256) {
+    const int grid_blocks = resident_blocks(kernel, variant, lds, keep, threads);
+    const int waves_per_block = threads / 64;
     // Small batches: one-tile units, so that more waves get work (a launch
     // wants several units per resident wave to balance the long rays).
     P.unit_rays = kUnitRays;
-    if (static_cast<int64_t>(P.n_rays) < static_cast<int64_t>(kUnitRays) * 4 * 4 * grid_blocks)
+    if (static_cast<int64_t>(P.n_rays) < static_cast<int64_t>(kUnitRays) * 4 * waves_per_block * grid_blocks)
         P.unit_rays = kSmallUnitRays;
     P.n_units = (P.n_rays + P.unit_rays - 1u) / P.unit_rays;
-    int64_t blocks = (static_cast<int64_t>(P.n_chunks) + 3) / 4;
+    int64_t blocks = (static_cast<int64_t>(P.n_chunks) + waves_per_block - 1) / waves_per_block;
     if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds, stream, P);
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
     return NAVI_OK;
@@ -1495,6 +1561,14 @@ int enqueue_relaid(void (*kernel)(RelaidParams), RelaidParams P, int variant, si
 // table, whose planes and scene table fit `budget` bytes; 0 if none does.
 int plane_depth_for(int32_t n_scenes, uint32_t D, size_t budget) {
     for (int p = D < 6 ? static_cast<int>(D) : 6; p >= 4 && p + 2 >= static_cast<int>(D); --p)
+        if (static_cast<size_t>(n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) return p;
+    return 0;
+}
+
+// The deepest split-plane depth P in (D, min(D + 2, 8)] whose planes and scene
+// table fit `budget` bytes; 0 if none does.
+int plane_depth_wide(int32_t n_scenes, uint32_t D, size_t budget) {
+    for (int p = D + 2 < 8 ? static_cast<int>(D) + 2 : 8; p > static_cast<int>(D); --p)
         if (static_cast<size_t>(n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) return p;
     return 0;
 }
@@ -1513,31 +1587,59 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
     const bool poses = P.local_dirs != nullptr;
     if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
 
-    // the fast kernel: planes that fit eight workgroups per CU
-    const int pf = plane_depth_for(P.n_scenes, D, kFastLds);
+    // the fast kernel: planes two levels below the table in two 1024-thread
+    // workgroups per CU, else planes that fit eight 256-thread workgroups
     P.after_fast = 0u;
-    if (pf != 0 && P.queue != nullptr && P.small_tables && P.max_distance < kOutsideDomain) {
+    if (P.queue != nullptr && P.small_tables && P.max_distance < kOutsideDomain) {
         RelaidParams F = P;
-        size_t lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pf) * sizeof(float));
-        F.stage = (F.out_steps == nullptr && lds + kStageLds <= kFastLds) ? 1u : 0u;
-        if (F.stage) lds += kStageLds;
         void (*fast)(RelaidParams) = nullptr;
-#define NAVI_FAST(d, p) (poses ? trace_fast_kernel<d, p, true> : trace_fast_kernel<d, p, false>)
-        switch (pf * 8 + static_cast<int>(D)) {
-            case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
-            case 4 * 8 + 5: fast = NAVI_FAST(5, 4); break;
-            case 4 * 8 + 6: fast = NAVI_FAST(6, 4); break;
-            case 5 * 8 + 5: fast = NAVI_FAST(5, 5); break;
-            case 5 * 8 + 6: fast = NAVI_FAST(6, 5); break;
-            case 5 * 8 + 7: fast = NAVI_FAST(7, 5); break;
-            case 6 * 8 + 6: fast = NAVI_FAST(6, 6); break;
-            case 6 * 8 + 7: fast = NAVI_FAST(7, 6); break;
-            default: break;
-        }
+        size_t lds = 0;
+        int threads = kWideThreads;
+        int variant = 0;
+        const bool wide = F.n_rays >= g_wide_min_rays.load(std::memory_order_relaxed);
+        const int pw = wide ? plane_depth_wide(F.n_scenes, D, kFastLdsWide) : 0;
+        if (pw != 0) {
+            lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pw) * sizeof(float));
+            F.stage = (F.out_steps == nullptr && lds + stage_lds(kWideThreads) <= kFastLdsWide) ? 1u : 0u;
+            if (F.stage) lds += stage_lds(kWideThreads);
+#define NAVI_FAST(d, p) \
+    (poses ? trace_fast_kernel<d, p, true, kWideThreads> : trace_fast_kernel<d, p, false, kWideThreads>)
+            switch (pw * 8 + static_cast<int>(D)) {
+                case 5 * 8 + 4: fast = NAVI_FAST(4, 5); break;
+                case 6 * 8 + 4: fast = NAVI_FAST(4, 6); break;
+                case 6 * 8 + 5: fast = NAVI_FAST(5, 6); break;
+                case 7 * 8 + 5: fast = NAVI_FAST(5, 7); break;
+                case 7 * 8 + 6: fast = NAVI_FAST(6, 7); break;
+                case 8 * 8 + 6: fast = NAVI_FAST(6, 8); break;
+                case 8 * 8 + 7: fast = NAVI_FAST(7, 8); break;
+                default: break;
+            }
 #undef NAVI_FAST
+            variant = 2 * (pw * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 2048;
+        }
+        const int pf = fast == nullptr ? plane_depth_for(F.n_scenes, D, kFastLds) : 0;
+        if (pf != 0) {
+            threads = 256;
+            lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pf) * sizeof(float));
+            F.stage = (F.out_steps == nullptr && lds + kStageLds <= kFastLds) ? 1u : 0u;
+            if (F.stage) lds += kStageLds;
+#define NAVI_FAST(d, p) (poses ? trace_fast_kernel<d, p, true, 256> : trace_fast_kernel<d, p, false, 256>)
+            switch (pf * 8 + static_cast<int>(D)) {
+                case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
+                case 4 * 8 + 5: fast = NAVI_FAST(5, 4); break;
+                case 4 * 8 + 6: fast = NAVI_FAST(6, 4); break;
+                case 5 * 8 + 5: fast = NAVI_FAST(5, 5); break;
+                case 5 * 8 + 6: fast = NAVI_FAST(6, 5); break;
+                case 5 * 8 + 7: fast = NAVI_FAST(7, 5); break;
+                case 6 * 8 + 6: fast = NAVI_FAST(6, 6); break;
+                case 6 * 8 + 7: fast = NAVI_FAST(7, 6); break;
+                default: break;
+            }
+#undef NAVI_FAST
+            variant = 2 * (pf * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 1024;
+        }
         if (fast != nullptr) {
-            const int variant = 2 * (pf * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 1024;
-            const int code = enqueue_relaid(fast, F, variant, lds, !no_alloc, stream);
+            const int code = enqueue_relaid(fast, F, variant, lds, !no_alloc, stream, threads);
             if (code != NAVI_OK) return code;
             P.after_fast = 1u;
         }
@@ -1637,6 +1739,8 @@ extern "C" int navi_device_init(void) {
     if (code != NAVI_OK) return code;
     return init_device_locked(dev);
 }
+
+extern "C" uint64_t navi_set_wide_min_rays(uint64_t n_rays) { return navi::g_wide_min_rays.exchange(n_rays); }
 
 extern "C" int navi_trace_relaid_noalloc(const uint32_t* records, uint64_t n_records,
                                          const navi_relaid_scene* scenes, int32_t n_scenes,

@@ -151,6 +151,20 @@ def test_every_declared_symbol_is_exported():
     assert re.fullmatch(r"\d+\.\d+\.\d+", _native.version())
 
 
+def test_wide_min_rays_knob_without_a_gpu():
+    """navi_set_wide_min_rays is host-only: it swaps the launch-shape threshold
+    (default 2^19 rays) and returns the previous one."""
+    prev = _native.set_wide_min_rays(12345)
+    try:
+        assert prev == 1 << 19
+        assert _native.set_wide_min_rays(0) == 12345
+        assert _native.set_wide_min_rays((1 << 64) - 1) == 0
+    finally:
+        _native.set_wide_min_rays(prev)
+    with pytest.raises(ValueError):
+        _native.set_wide_min_rays(-1)
+
+
 def test_c_abi_rejects_bad_arguments_without_a_gpu():
     lib = _native.lib()
     f3 = _native.float3

@@ -445,6 +445,41 @@ def test_relaid_every_table_depth(gpu, corpus, depth):
     _compare(_run(res, env_scene, o, d, 64, 5.0), ref, 5.0, f"depth{depth}/narrow")
 
 
+@pytest.mark.parametrize("n,depth,planes", [(16, 4, 6), (16, 5, 7), (16, 6, 8), (16, 7, 8), (30, 6, 7),
+                                            (60, 5, 6), (100, 4, 5)])
+def test_relaid_wide_workgroups_planes_below_the_tables(gpu, corpus, n, depth, planes):
+    """The 1024-thread fast kernel (forced for these small batches with
+    navi_set_wide_min_rays): split planes one or two levels below the cell tables,
+    whose levels between take their octants from the plane index. Every instance,
+    canonical rays with step counts and random rays from in and around the domains
+    (faces of cells and of the cached prefix cell crossed often), against the
+    oracle."""
+    from navi_amd import _native
+    from navi_amd.multiscene import ResidentScenes, wide_plane_depth
+
+    assert wide_plane_depth(n, depth) == planes
+    many = [(corpus[i % 4].words, corpus[i % 4].bbox_min_list, corpus[i % 4].bbox_max) for i in range(n)]
+    words = [s[0] for s in many]
+    bounds = [list(s[1]) + list(s[2]) for s in many]
+    prev = _native.set_wide_min_rays(0)
+    try:
+        res = ResidentScenes(many, table_depth=depth)
+        env_scene, o, d = _rays(corpus, 20, 16, 16, seed=70 + depth)
+        env_scene = (env_scene + 4 * np.arange(20, dtype=np.int32)) % n
+        ref = _oracle_multi(words, bounds, env_scene, o, d, 200, 30.0)
+        _compare(_run(res, env_scene, o, d, 200, 30.0, elevation_bins=16), ref, 30.0, f"wide{planes}/depth{depth}")
+        rng = np.random.default_rng(n * 7 + depth)
+        lo = np.array([bounds[s][:3] for s in env_scene]) - 2.0
+        hi = np.array([bounds[s][3:] for s in env_scene]) + 2.0
+        o = rng.uniform(lo[:, None, :], hi[:, None, :], (20, 400, 3)).astype(np.float32)
+        d = rng.normal(size=(20, 400, 3))
+        d = (d / np.linalg.norm(d, axis=-1, keepdims=True)).astype(np.float32)
+        ref = _oracle_multi(words, bounds, env_scene, o, d, 300, 29.0)
+        _compare(_run(res, env_scene, o, d, 300, 29.0), ref, 29.0, f"wide{planes}/depth{depth}/random")
+    finally:
+        _native.set_wide_min_rays(prev)
+
+
 @pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (30, 6, 5), (60, 5, 4), (60, 6, 4), (100, 6, 4),
                                             (120, 5, 0)])
 def test_relaid_tables_below_the_planes(gpu, corpus, n, depth, planes):

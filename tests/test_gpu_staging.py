@@ -6,7 +6,8 @@ of skipped envs) untouched. Called through the C ABI on a pool of monotone scene
 fast march's launches), for 8x8 tiles and for linear ray order, explicit rays and
 rays from poses, env orders with skipped entries, unknown scene ids, a batch with
 many tiles per wave (slots evicted while rays of their tile still march) and the
-no-allocation entry point; one staged launch is checked against the oracle too.
+no-allocation entry point; one staged launch is checked against the oracle too. Every
+test runs in both launch shapes (256- and 1024-thread workgroups).
 """
 
 from __future__ import annotations
@@ -28,12 +29,19 @@ def _say(msg: str) -> None:
     print(f"[test_gpu_staging] {msg}", file=sys.stderr, flush=True)
 
 
-@pytest.fixture(scope="module")
-def pool(gpu):
+@pytest.fixture(scope="module", params=["wg256", "wg1024"])
+def pool(gpu, request):
+    """The scene pool; the module runs twice: the default launch shape for these
+    small batches (256-thread workgroups, planes above the tables) and the wide one
+    (1024-thread workgroups, planes two levels below the tables), forced through
+    navi_set_wide_min_rays."""
     import torch
 
     from navi_amd import _native
     from navi_amd import scenes as S
+
+    prev = _native.set_wide_min_rays(0 if request.param == "wg1024" else 1 << 19)
+    request.addfinalizer(lambda: _native.set_wide_min_rays(prev))
 
     scenes = [S.rooms(seed=3, resolution=128), S.cluttered(seed=2, resolution=128), S.box_room(seed=4, resolution=64)]
     for sc in scenes:
