@@ -355,10 +355,11 @@ __device__ __forceinline__ Sched sched_init(const RelaidParams& P) {
 
 // Work indices for the wave's idle lanes (`need`, n_need of them; `rank` =
 // idle lanes below this one): this lane's index, or 0xffffffff for none.
+template <bool kQueued = false>
 __device__ __forceinline__ uint32_t claim(const RelaidParams& P, Sched& S, uint32_t n_need, uint32_t rank,
                                           uint32_t lane) {
     uint32_t q = 0xffffffffu;
-    if (P.queue == nullptr) {
+    if (!kQueued && P.queue == nullptr) {
         const uint32_t sq = S.seq_next + rank;
         if (sq < S.seq_end) q = (S.wave + (sq >> 6) * S.n_waves) * 64u + (sq & 63u);
         S.seq_next += n_need;
@@ -450,6 +451,17 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
     return 1;
 }
 
+// The launch parameters as the kernel-argument segment holds them (the
+// kernels' first argument). The march reads through this the fields only its
+// rare paths need (refill, write-out): loads from that segment are invariant,
+// so the compiler reloads them where they are used instead of keeping them in
+// scalar registers across the loop (where they crowded out the step's own:
+// 30 scalar registers spilled into vector-register lanes, one vector
+// operation per read, four of them on every step for the table's resource).
+__device__ __forceinline__ const RelaidParams& reload_params() {
+    return *(const RelaidParams*)__builtin_amdgcn_kernarg_segment_ptr();  // address-space cast
+}
+
 // The fast march: launches whose scenes all have split planes in LDS, tame
 // boxes, no record deeper than 30 levels and no negative leaf distance, with
 // cell tables below 4 GiB (every scene the library's compiler writes) and a
@@ -460,7 +472,7 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
 // leaf-run step (tame boxes) and the box faces behind the ray (below). The
 // step's conditions are wave masks, so its path has no short-circuit branches,
 // and the cell table is read through a buffer resource (32-bit offsets).
-template <int kDepth, int kPD, bool kPoses>
+template <int kDepth, int kPD, bool kPoses, bool kQueued>
 __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
                                            const float* lds_planes, uint32_t* lds_stage) {
     static_assert(kPD >= 4 && kPD <= 8 && kDepth >= 4 && kDepth <= kPD + 2 && kDepth <= 7,
@@ -522,6 +534,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
     // tile's slot, or 0 (the ray stores its own outputs; the staging area lies
     // above the scene table, never at address 0) ----
     const bool stage = P.stage != 0u;
+    const bool out_steps = P.out_steps != nullptr;
     uint32_t tag = 0, ring = 0;
     uint32_t st0 = kNoTile, st1 = kNoTile;
     uint32_t* const my_stage = lds_stage + (threadIdx.x >> 6) * (kStageSlots * kStageWords);
@@ -535,10 +548,11 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         const uint32_t tv = sl[flush_pos];
         sl[64u + flush_pos] = kStageEmpty;
         if (sv != kStageEmpty) {
+            const RelaidParams& RP = reload_params();
             int32_t env = 0;
-            const uint32_t r = ray_of(P, tile * 64u + flush_pos, env);
-            __builtin_nontemporal_store(__uint_as_float(tv), &P.out_d[r]);
-            __builtin_nontemporal_store(static_cast<int32_t>(sv), &P.out_s[r]);
+            const uint32_t r = ray_of(RP, tile * 64u + flush_pos, env);
+            __builtin_nontemporal_store(__uint_as_float(tv), &RP.out_d[r]);
+            __builtin_nontemporal_store(static_cast<int32_t>(sv), &RP.out_s[r]);
         }
     };
     if (stage) {
@@ -560,10 +574,11 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         if ((n_need >= kRefillMinFast || n_need == 64u) && !sched.exhausted) {
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
-            const uint32_t q = claim(P, sched, n_need, rank, lane);
+            const RelaidParams& RP = reload_params();
+            const uint32_t q = claim<kQueued>(RP, sched, n_need, rank, lane);
             RayStart R;
             bool fresh = false;
-            if (__builtin_amdgcn_inverse_ballot_w64(need) && start_ray<kPoses>(P, q, R) == 1) {
+            if (__builtin_amdgcn_inverse_ballot_w64(need) && start_ray<kPoses>(RP, q, R) == 1) {
                 fresh = true;
                 ray = R.ray;
                 scene = R.scene;
@@ -650,9 +665,14 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         // (the leaf lies in the domain)
         const uint64_t m_hit_lf = wave_mask(qx <= lfx) & wave_mask(qy <= lfy) & wave_mask(qz <= lfz);
         const bool descending = lane_in(m_ray & m_dom & ~m_hit_lf);
-        // the faces ahead (mirrored) of the box a descent ends in
-        float hx = qx, hy = qy, hz = qz;
-        uint32_t slot = 0;  // an internal slot: no outcome for lanes that do not descend
+        // the faces ahead (mirrored) of the box a descent ends in; lanes that do
+        // not descend keep the void marker and faces at +inf, so their exit
+        // quotients are NaN, the exit distance is the outside-domain distance
+        // (fminf drops NaN), and a lane outside the domain takes that step as
+        // a void step (a leaf-cache lane takes its leaf's distance first)
+        constexpr float kInf = __builtin_inff();
+        float hx = kInf, hy = kInf, hz = kInf;
+        uint32_t slot = kSlotVoid;
 
         if (descending) {
             const float px = mirror(qx, dx), py = mirror(qy, dy), pz = mirror(qz, dz);
@@ -749,14 +769,21 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             pre_cell = save ? saved : pre_cell;
 
             if constexpr (kPD > D) {
+                static_assert((kFW == 8u || kFW == 10u) && kPD <= D + 2, "octant gather: 8- or 10-bit fields, bits 0-1");
                 // ---- from the table down to depth kPD: the octants are the
                 // plane index's bits (kernel.cu:165-176 picks the same ones:
                 // the depth-kPD cell lies in the box each split leads to) ----
 #pragma unroll
                 for (uint32_t l = D; l < static_cast<uint32_t>(kPD); ++l) {
                     if (slot < kSlotBadChild) {  // an internal node at depth l
-                        const uint32_t b = kPD - 1u - l;
-                        const uint32_t oct = ((jx >> b) & 1u) | (((jy >> b) & 1u) << 1) | (((jz >> b) & 1u) << 2);
+                        // the octant: bit b of each index field of `packed`, gathered
+                        // by one 24-bit multiply (x to bit 22, y to 23, z to 24;
+                        // every other product bit lies apart from those three)
+                        const uint32_t b = kPD - 1u - l;  // 0 or 1 (the loop is unrolled)
+                        const uint32_t kBits = kOnes << b;
+                        const uint32_t kGather =
+                            (1u << (22u - b)) | (1u << (23u - kFW - b)) | (1u << (24u - 2u * kFW - b));
+                        const uint32_t oct = __builtin_amdgcn_ubfe(__umul24(packed & kBits, kGather), 22u, 3u);
                         slot = navi_struct_load_b32(records, static_cast<int32_t>((slot << 3) | oct), 0, 0, 0);
                         depth = l + 1u;
                     }
@@ -812,9 +839,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         // hit: their semantic is 0)
         // (inverse ballots are convergent: read them outside the conditional
         // expression, which then stays a chain of selects)
-        const bool on_leaf = lane_in(m_leaf), outside = lane_in(~m_dom);
-        const float dist =
-            slot == kSlotVoid ? void_d : (on_leaf ? leaf_d : (outside ? kOutsideDomain : __builtin_nanf("")));
+        const bool on_leaf = lane_in(m_leaf);
+        const float dist = on_leaf ? leaf_d : (slot == kSlotVoid ? void_d : __builtin_nanf(""));
         const uint64_t m_hit = m_leaf & wave_mask(leaf_s != 0) & wave_mask(dist < P.hit_eps);
         const float t_next = t + dist;
         uint64_t m_fin = m_ray & (wave_mask(slot == kSlotFault) | m_hit | wave_mask(t_next > P.max_distance) |
@@ -846,10 +872,14 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 e[64] = static_cast<uint32_t>(sem);
             } else {
                 // non-temporal: lines of these scattered 4-byte stores do not stay in L2
-                __builtin_nontemporal_store(t, &P.out_d[ray]);
-                __builtin_nontemporal_store(sem, &P.out_s[ray]);
+                const RelaidParams& RP = reload_params();
+                __builtin_nontemporal_store(t, &RP.out_d[ray]);
+                __builtin_nontemporal_store(sem, &RP.out_s[ray]);
             }
-            if (P.out_steps) P.out_steps[ray] = step;
+            if (out_steps) {
+                const RelaidParams& RP = reload_params();
+                RP.out_steps[ray] = step;
+            }
         }
     }
     if (stage) {
@@ -1383,7 +1413,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) v
     const bool fast = fast_applies(P, c);
     if (blockIdx.x == 0 && threadIdx.x == 0) P.queue[2] = fast ? 1u : 0u;
     if (!fast) return;
-    march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
+    march_fast<kDepth, kPD, kPoses, true>(P, lds_scenes, lds_planes,
                                     reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
     rearm_queue(P);
 }
@@ -1403,7 +1433,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     const LaunchConds c = stage_scenes<kPD>(P, lds_scenes, lds_planes);
     if constexpr (kPlanes) {
         if (fast_applies(P, c))
-            march_fast<kDepth, kPD, kPoses>(P, lds_scenes, lds_planes,
+            march_fast<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes,
                                             reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
         else
             march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, c.tame, c.shallow, c.planes, c.void_cache);
