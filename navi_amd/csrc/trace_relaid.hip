@@ -945,9 +945,10 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
             // idle lanes below this one (mbcnt: set bits of `need` under the lane)
             const uint32_t rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(need >> 32),
                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(need), 0u));
-            const uint32_t q = claim(P, sched, n_need, rank, lane);
+            const RelaidParams& RP = reload_params();
+            const uint32_t q = claim(RP, sched, n_need, rank, lane);
             RayStart R;
-            if (!has_ray && start_ray<kPoses>(P, q, R) == 1) {
+            if (!has_ray && start_ray<kPoses>(RP, q, R) == 1) {
                 ray = R.ray;
                 scene = R.scene;
                 ox = R.ox;
@@ -1323,9 +1324,10 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
         }
         if (finish) {
             // non-temporal: lines of these scattered 4-byte stores do not stay in L2
-            __builtin_nontemporal_store(t, &P.out_d[ray]);
-            __builtin_nontemporal_store(sem, &P.out_s[ray]);
-            if (P.out_steps) P.out_steps[ray] = step;
+            const RelaidParams& RP = reload_params();
+            __builtin_nontemporal_store(t, &RP.out_d[ray]);
+            __builtin_nontemporal_store(sem, &RP.out_s[ray]);
+            if (RP.out_steps) RP.out_steps[ray] = step;
         }
     }
 }
@@ -1595,10 +1597,11 @@ int plane_depth_for(int32_t n_scenes, uint32_t D, size_t budget) {
     return 0;
 }
 
-// The deepest split-plane depth P in (D, min(D + 2, 8)] whose planes and scene
-// table fit `budget` bytes; 0 if none does.
+// The deepest split-plane depth P in [max(4, D - 2), min(D + 2, 8)] whose
+// planes and scene table fit `budget` bytes; 0 if none does.
 int plane_depth_wide(int32_t n_scenes, uint32_t D, size_t budget) {
-    for (int p = D + 2 < 8 ? static_cast<int>(D) + 2 : 8; p > static_cast<int>(D); --p)
+    const int lo = D > 6 ? static_cast<int>(D) - 2 : 4;
+    for (int p = D + 2 < 8 ? static_cast<int>(D) + 2 : 8; p >= lo; --p)
         if (static_cast<size_t>(n_scenes) * (sizeof(SceneLds) + scene_stride(p) * sizeof(float)) <= budget) return p;
     return 0;
 }
@@ -1635,12 +1638,21 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
 #define NAVI_FAST(d, p) \
     (poses ? trace_fast_kernel<d, p, true, kWideThreads> : trace_fast_kernel<d, p, false, kWideThreads>)
             switch (pw * 8 + static_cast<int>(D)) {
+                case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
                 case 5 * 8 + 4: fast = NAVI_FAST(4, 5); break;
                 case 6 * 8 + 4: fast = NAVI_FAST(4, 6); break;
+                case 4 * 8 + 5: fast = NAVI_FAST(5, 4); break;
+                case 5 * 8 + 5: fast = NAVI_FAST(5, 5); break;
                 case 6 * 8 + 5: fast = NAVI_FAST(5, 6); break;
                 case 7 * 8 + 5: fast = NAVI_FAST(5, 7); break;
+                case 4 * 8 + 6: fast = NAVI_FAST(6, 4); break;
+                case 5 * 8 + 6: fast = NAVI_FAST(6, 5); break;
+                case 6 * 8 + 6: fast = NAVI_FAST(6, 6); break;
                 case 7 * 8 + 6: fast = NAVI_FAST(6, 7); break;
                 case 8 * 8 + 6: fast = NAVI_FAST(6, 8); break;
+                case 5 * 8 + 7: fast = NAVI_FAST(7, 5); break;
+                case 6 * 8 + 7: fast = NAVI_FAST(7, 6); break;
+                case 7 * 8 + 7: fast = NAVI_FAST(7, 7); break;
                 case 8 * 8 + 7: fast = NAVI_FAST(7, 8); break;
                 default: break;
             }

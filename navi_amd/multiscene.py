@@ -60,11 +60,11 @@ WIDE_PLANE_LDS_BYTES = 81920  # kFastLdsWide: two 1024-thread workgroups per CU
 
 def wide_plane_depth(n_scenes: int, table_depth: int) -> int:
     """The split-plane depth of the 1024-thread fast kernel (launch_relaid's
-    ``plane_depth_wide``): the deepest P in (D, min(D + 2, 8)] whose planes and scene
-    table fit ``WIDE_PLANE_LDS_BYTES``; 0 when none does (such launches take the
-    256-thread workgroups). Launches of fewer rays than ``navi_set_wide_min_rays``
+    ``plane_depth_wide``): the deepest P in [max(4, D - 2), min(D + 2, 8)] whose planes
+    and scene table fit ``WIDE_PLANE_LDS_BYTES``; 0 when none does (such launches take
+    the 256-thread workgroups). Launches of fewer rays than ``navi_set_wide_min_rays``
     (default 2^19) take the 256-thread workgroups whatever this says."""
-    for p in range(min(table_depth + 2, 8), table_depth, -1):
+    for p in range(min(table_depth + 2, 8), max(4, table_depth - 2) - 1, -1):
         if n_scenes * (32 + _plane_bytes(p)) <= WIDE_PLANE_LDS_BYTES:
             return p
     return 0

@@ -446,14 +446,15 @@ def test_relaid_every_table_depth(gpu, corpus, depth):
 
 
 @pytest.mark.parametrize("n,depth,planes", [(16, 4, 6), (16, 5, 7), (16, 6, 8), (16, 7, 8), (30, 6, 7),
-                                            (60, 5, 6), (100, 4, 5)])
-def test_relaid_wide_workgroups_planes_below_the_tables(gpu, corpus, n, depth, planes):
+                                            (60, 5, 6), (100, 4, 5), (64, 6, 6), (128, 6, 5), (200, 6, 4),
+                                            (100, 5, 5), (200, 5, 4), (200, 4, 4), (40, 7, 7)])
+def test_relaid_wide_workgroups(gpu, corpus, n, depth, planes):
     """The 1024-thread fast kernel (forced for these small batches with
     navi_set_wide_min_rays): split planes one or two levels below the cell tables,
-    whose levels between take their octants from the plane index. Every instance,
-    canonical rays with step counts and random rays from in and around the domains
-    (faces of cells and of the cached prefix cell crossed often), against the
-    oracle."""
+    whose levels between take their octants from the plane index, or at or above
+    them for launches with many scenes. Every instance, canonical rays with step
+    counts and random rays from in and around the domains (faces of cells and of
+    the cached prefix cell crossed often), against the oracle."""
     from navi_amd import _native
     from navi_amd.multiscene import ResidentScenes, wide_plane_depth
 
