@@ -6,7 +6,9 @@
 // Execution model (CDNA4, wave64):
 //   * two kernels: the fast march (monotone, tame, shallow scenes with split
 //     planes, the library compiler's) alone in trace_fast_kernel at eight
-//     waves per SIMD, everything in trace_relaid_kernel at seven; a launch
+//     waves per SIMD, in two 1024-thread workgroups per CU for launches of at
+//     least 2^19 rays (planes up to two levels below the cell table) or eight
+//     256-thread ones, everything in trace_relaid_kernel at seven; a launch
 //     enqueues the first when its planes fit, the second after it (returning
 //     at once when the first traced the launch), see launch_relaid;
 //   * persistent waves: the grid holds as many workgroups as the chip keeps
@@ -219,7 +221,7 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 // x, y and z and a pad float, the offsets -lo * scale - 0.25 of x, y and z and
 // a pad float, then per axis the n + 1 planes P_0 = lo, ..., P_n = hi of the
 // n = 2^P depth-P cells and a pad float, the scene's block rounded up to 16
-// bytes. A launch stages the deepest P (at most 6, at most
+// bytes. The general kernel stages the deepest P (at most 6, at most
 // two levels above the cell table) whose scene table and planes fit kPlaneLds
 // bytes (seven 256-thread workgroups, 7 waves per SIMD, within a CU's 160 KiB
 // of LDS); failing that, the deepest that fits kPlaneLdsWide (five
@@ -228,7 +230,8 @@ constexpr int32_t kMaxScenes = 1024;  // 32 KiB of LDS
 // and planes at 4 waves lose to none.
 constexpr size_t kPlaneLds = 22528;
 constexpr size_t kPlaneLdsWide = 32512;
-// The fast kernel's LDS per workgroup: eight 256-thread workgroups per CU.
+// The fast kernel's LDS per workgroup in its 256-thread shape: eight
+// workgroups per CU (planes at most 6 levels, at most two above the table).
 constexpr size_t kFastLds = 20480;
 // The wide fast kernel: two 1024-thread workgroups per CU (eight waves per
 // SIMD), each with half the CU's 160 KiB of LDS, room for split planes two
@@ -330,8 +333,9 @@ __device__ __forceinline__ uint32_t plane_cell(float p, float off, float scale, 
 
 // kPD > 0: the scenes' split planes of the first kPD levels staged in LDS and
 // kDepth the cell-table depth (kPD <= kDepth <= kPD + 2: a depth-kDepth cell is
-// kDepth - kPD splits below its depth-kPD cell); kPD = 0: no planes, the table
-// depth is P.cell_depth and cells come from splits.
+// kDepth - kPD splits below its depth-kPD cell; in the fast march also
+// kDepth < kPD: the table index is the plane index shifted right); kPD = 0: no
+// planes, the table depth is P.cell_depth and cells come from splits.
 // Wave-uniform work distribution of one wave: a static sequence of 64-ray
 // chunks (wave, wave + n_waves, ...) without a queue, else work units claimed
 // from the queue, `unit_used` rays of `unit` handed out so far.
@@ -1401,8 +1405,8 @@ __device__ __forceinline__ void rearm_queue(const RelaidParams& P) {
 
 // The fast march in a kernel of its own, at eight waves per SIMD (64 vector
 // registers; the general march needs 72, and six waves instead of seven cost
-// the fast march 8% where eight gain it 5%). Launched first when its LDS fits
-// eight workgroups per CU and the launch has a work queue; it records in the
+// the fast march 8% where eight gain it 5%). Launched first when its planes
+// fit one of its two shapes and the launch has a work queue; it records in the
 // queue's third word whether the fast march applied and returns at once when
 // it does not (the general kernel, launched next, then traces the launch).
 template <int kDepth, int kPD, bool kPoses, int kThreads>
@@ -1421,7 +1425,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) v
 }
 
 // Both marches, at seven waves per SIMD: the fast march where it applies (for
-// launches whose LDS does not fit the fast kernel's eight workgroups), else
+// launches whose planes fit neither of the fast kernel's shapes), else
 // the general one. Launched after trace_fast_kernel (after_fast), it returns at
 // once when that one traced the launch.
 template <int kDepth, int kPD, bool kPoses>
@@ -1607,8 +1611,8 @@ int plane_depth_wide(int32_t n_scenes, uint32_t D, size_t budget) {
 }
 
 // queue: the counter words to use (no_alloc), or null to take the stream's.
-// A launch whose planes fit kFastLds (and that has a queue, a range below the
-// outside-domain distance and small tables) enqueues trace_fast_kernel, then
+// A launch whose planes fit kFastLdsWide or kFastLds (and that has a queue, a
+// range below the outside-domain distance and small tables) enqueues trace_fast_kernel, then
 // trace_relaid_kernel with after_fast, which returns at once when the fast
 // kernel traced it (every other launch: trace_relaid_kernel alone).
 int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = nullptr) {
@@ -1620,8 +1624,9 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
     const bool poses = P.local_dirs != nullptr;
     if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
 
-    // the fast kernel: planes two levels below the table in two 1024-thread
-    // workgroups per CU, else planes that fit eight 256-thread workgroups
+    // the fast kernel: for large launches planes up to two levels below the
+    // table in two 1024-thread workgroups per CU, else planes that fit eight
+    // 256-thread workgroups
     P.after_fast = 0u;
     if (P.queue != nullptr && P.small_tables && P.max_distance < kOutsideDomain) {
         RelaidParams F = P;
