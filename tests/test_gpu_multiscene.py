@@ -481,6 +481,38 @@ def test_relaid_wide_workgroups(gpu, corpus, n, depth, planes):
         _native.set_wide_min_rays(prev)
 
 
+def test_fast_kernel_256_thread_shape(gpu, corpus):
+    """The 256-thread fast kernel: launches of at least 2^19 rays below a raised
+    wide threshold (navi_set_wide_min_rays). 64 envs x 128x64 rays (524,288) over
+    the four scenes, staged (no step counts) and with step counts, against the
+    oracle; smaller launches take the combined kernel alone and the GPU suite's
+    other tests cover it."""
+    import torch
+
+    from navi_amd import _native
+    from navi_amd.multiscene import ResidentScenes
+
+    res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus])
+    env_scene, o, d = _rays(corpus, 64, 128, 64, seed=91)
+    assert o.shape[0] * o.shape[1] == 1 << 19
+    ref = _oracle_multi([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus],
+                        env_scene, o, d, 256, 30.0)
+    prev = _native.set_wide_min_rays(1 << 30)
+    try:
+        _compare(_run(res, env_scene, o, d, 256, 30.0, elevation_bins=64), ref, 30.0, "wg256/steps")
+        dev = res.device
+        out_d = torch.full(o.shape[:2], -7.0, device=dev)
+        out_s = torch.full(o.shape[:2], -7, device=dev, dtype=torch.int32)
+        res.cast_rays(torch.from_numpy(env_scene).to(dev), torch.from_numpy(np.ascontiguousarray(o)).to(dev),
+                      torch.from_numpy(np.ascontiguousarray(d)).to(dev), out_d, out_s, 256, 30.0, elevation_bins=64)
+        torch.cuda.synchronize()
+        gd, gs = out_d.cpu().numpy(), out_s.cpu().numpy()
+        assert np.array_equal(gs, ref["semantic"]), "wg256/staged: semantics"
+        assert np.array_equal(gd.view(np.uint32), ref["distance"].view(np.uint32)), "wg256/staged: distance bits"
+    finally:
+        _native.set_wide_min_rays(prev)
+
+
 @pytest.mark.parametrize("n,depth,planes", [(27, 7, 5), (30, 6, 5), (60, 5, 4), (60, 6, 4), (100, 6, 4),
                                             (120, 5, 0)])
 def test_relaid_tables_below_the_planes(gpu, corpus, n, depth, planes):
