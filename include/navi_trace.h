@@ -32,13 +32,56 @@ extern "C" {
 /*
  * Per-device set-up (no reference counterpart: the reference kernel keeps no
  * state between launches, kernel.cu:311-326). On the current device,
- * allocates and clears the record-layout tracers' work-queue counters (32 KiB,
- * kept until the process ends) and looks up the device's copy of
+ * allocates and clears the record-layout tracers' work-queue counters (64 KiB:
+ * 4096 pairs of four words, kept until the process ends), creates the events
+ * that guard the reserve pairs (below), and looks up the device's copy of
  * navi_trace_relaid_noalloc's static scratch; idempotent and thread-safe. Call
  * it where allocation and a device wait are acceptable (scene load), so that
  * no later launch on this device allocates or waits.
+ *
+ * Work-queue pairs: an eager launch uses its stream's pair (one per host
+ * thread for hipStreamPerThread), kept for the life of the process; a launch
+ * recorded into a graph gets a pair of its own, given back when that graph and
+ * every executable graph instantiated from it are destroyed (executable graphs
+ * of one capture share it: do not replay two of them at once). When the
+ * 4032 table pairs are in use, an eager launch leases one of 64 reserve pairs,
+ * free again once the launch has completed (an event recorded after it);
+ * only when all of those are in flight does a launch run without a queue (the
+ * general march on a static schedule, correct but slower).
+ * navi_last_launch reports which case a launch met.
  */
 int navi_device_init(void);
+
+/* What the calling thread's last tracer launch enqueued (no reference
+ * counterpart: the reference has one kernel, kernel.cu:311-326). */
+typedef struct navi_launch_info {
+    uint32_t kernels;      /* NAVI_KERNEL_* bits of the kernels enqueued */
+    uint32_t queue;        /* NAVI_QUEUE_* kind of work-queue pair the launch used */
+    int32_t pair;          /* index of that pair in the device's table, -1 for none / scratch */
+    uint32_t fast_planes;  /* split-plane depth staged by trace_fast_kernel (0: not enqueued) */
+    uint32_t planes;       /* split-plane depth staged by trace_relaid_kernel (0: none) */
+    uint32_t staged;       /* 1 when finished rays are staged per tile in LDS */
+    uint32_t waves;        /* waves of the tracing grid (trace_fast_kernel's when enqueued) */
+    uint64_t n_rays;
+} navi_launch_info;
+
+/* navi_launch_info.kernels. trace_fast_kernel runs the fast march when every
+ * scene of the launch qualifies (NAVI_SCENE_NONNEG_LEAVES, boxes below 2^100,
+ * no record deeper than 30 levels; the device checks the scene table) and
+ * otherwise hands the launch to trace_relaid_kernel, enqueued after it. */
+#define NAVI_KERNEL_FAST 1u         /* trace_fast_kernel */
+#define NAVI_KERNEL_FAST_WIDE 2u    /* ... in 1024-thread workgroups (two per CU) */
+#define NAVI_KERNEL_COMBINED 4u     /* trace_relaid_kernel (both marches, seven waves per SIMD) */
+#define NAVI_KERNEL_RAW 8u          /* the word-layout kernel (navi_cast_rays, navi_cast_rays_multi) */
+/* navi_launch_info.queue */
+#define NAVI_QUEUE_NONE 0u     /* no pair: static schedule, trace_fast_kernel not enqueued */
+#define NAVI_QUEUE_STREAM 1u   /* the stream's pair */
+#define NAVI_QUEUE_CAPTURE 2u  /* a pair of the graph being captured */
+#define NAVI_QUEUE_LEASE 3u    /* a reserve pair leased for this launch */
+#define NAVI_QUEUE_SCRATCH 4u  /* navi_trace_relaid_noalloc's static scratch */
+
+/* Copies the calling thread's last launch's info into *info (zeroes when none). */
+int navi_last_launch(navi_launch_info* info);
 
 /* Hit threshold of the reference tracer (projects/torch-sdf/cpp_src/kernel.cuh:7). */
 #define NAVI_DEFAULT_HIT_EPSILON 0.01f
@@ -97,19 +140,36 @@ int navi_cast_rays_multi(const uint64_t* pool, const navi_scene_desc* scenes, in
  * layout (host memory) into 32-byte records of eight u32 octant slots in
  * breadth-first order: 0x7fffffff void, 0x7ffffffe out-of-range child-table
  * word, 0x7ffffffd out-of-range child index (a fault only where the child is
- * examined, above the 32-level descent limit), bit 31
- * set = leaf inlined (bits 30..16 semantic, 15..0 fp16 distance), else a
- * record index. With out_records NULL only counts; otherwise writes up to
- * cap_records records. *root_slot is the root's slot value (0 = record 0, or
- * an inlined leaf). n_levels_prefix (optional, 8 entries) receives the number
- * of records at depth <= l. When no record lies deeper than 30 levels
- * (navi_record_depth <= 30) every 0x7ffffffd slot is written as 0x7ffffffe:
- * it is examined above the descent limit, where both fault. Returns
- * NAVI_E_LAYOUT for DAGs with a reachable leaf semantic above 0x7fff (trace
- * those with navi_cast_rays*).
+ * examined, above the 32-level descent limit), 0xffff0000 | i a leaf of
+ * semantic 0x7fff or above (entry i of the leaf table, navi_relayout_leaves),
+ * other values with bit 31 set a leaf inlined (bits 30..16 semantic, 15..0
+ * fp16 distance), else a record index. With out_records NULL only counts;
+ * otherwise writes up to cap_records records. *root_slot is the root's slot
+ * value (0 = record 0, or a leaf of a one-leaf DAG). n_levels_prefix
+ * (optional, 8 entries) receives the number of records at depth <= l. When no
+ * record lies deeper than 30 levels (navi_record_depth <= 30) every 0x7ffffffd
+ * slot is written as 0x7ffffffe: it is examined above the descent limit,
+ * where both fault. Returns NAVI_E_LAYOUT for DAGs with a reachable leaf of
+ * semantic 0x7fff or above: convert those with navi_relayout_leaves.
  */
 int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
                   uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix);
+
+/*
+ * navi_relayout with a leaf table for the leaves whose semantic does not fit
+ * the inline slot's 15 bits (the format's field is 16 bits, docs/GMDAG.md:
+ * 215,223): each distinct (semantic, distance) pair of semantic 0x7fff or
+ * above gets one u32 entry (semantic << 16) | fp16 distance, in order of first
+ * sight, and its leaves the slot 0xffff0000 | entry. *n_leaves receives the
+ * entry count (0 for a DAG without such leaves); with out_leaves non-NULL the
+ * entries are written (at most cap_leaves). At most 65536 entries per table
+ * (NAVI_E_LAYOUT beyond). Several scenes in one record pool share one table:
+ * concatenate the scenes' tables and add each scene's offset to the low 16
+ * bits of its 0xffff0000 slots (the pool's table holds at most 65536 entries).
+ */
+int navi_relayout_leaves(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
+                         uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix,
+                         uint32_t* out_leaves, uint32_t cap_leaves, uint32_t* n_leaves);
 
 /* One resident scene in the device layout (device memory, 48 bytes). Several
  * scenes share one record pool: scene records are concatenated and every child
@@ -131,8 +191,22 @@ typedef struct navi_relaid_scene {
  * root leaf) has its fp16 sign bit set, so distances never decrease along a
  * ray. When every scene of a launch has it (and its boxes are below 2^100),
  * the tracer skips the reference's void cache (kernel.cu:265-267), which then
- * only repeats what a fresh query finds. */
+ * only repeats what a fresh query finds. The tracer trusts the flag: set on a
+ * scene with a negative leaf it gives wrong distances. Compute it with
+ * navi_scene_flags. */
 #define NAVI_SCENE_NONNEG_LEAVES 1u
+
+/*
+ * The NAVI_SCENE_* flags a scene's records support (no reference counterpart;
+ * host memory): NAVI_SCENE_NONNEG_LEAVES when no leaf reachable from root_slot
+ * (nor a root leaf) has its fp16 sign bit set, a table leaf's in `leaves`
+ * (n_leaves entries; NULL and 0 for none). Pass the records and root_slot as
+ * navi_build_cell_table takes them. Unreachable
+ * records are not examined; out-of-range records and cycles end the walk
+ * without error (the tracer reports those rays as faults).
+ */
+int navi_scene_flags(const uint32_t* records, uint64_t n_records, uint32_t root_slot, const uint32_t* leaves,
+                     uint32_t n_leaves, uint32_t* flags);
 
 /*
  * Depth of a scene's record graph (no reference counterpart; host memory):
@@ -228,6 +302,41 @@ int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const n
                             int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                             void* stream);
 
+/* Arguments of navi_trace_relaid_ex (device pointers unless noted). */
+typedef struct navi_relaid_launch {
+    const uint32_t* records;           /* record pool, as navi_trace_relaid */
+    uint64_t n_records;
+    const uint32_t* leaves;            /* the pool's leaf table (navi_relayout_leaves), or NULL */
+    uint32_t n_leaves;                 /* its entries (0 for none) */
+    const navi_relaid_scene* scenes;
+    int32_t n_scenes;
+    const uint64_t* cell_tables;
+    int32_t table_depth;
+    const int32_t* env_scene;          /* [n_envs] or NULL (scene 0) */
+    const int32_t* env_order;          /* [n_envs] or NULL (in order) */
+    int64_t n_envs;
+    int64_t rays_per_env;
+    int32_t elevation_bins;
+    const float* origins;              /* [n_rays][3] explicit rays, or NULL with local_dirs */
+    const float* dirs;
+    const float* local_dirs;           /* rays from poses, as navi_trace_relaid_poses */
+    const float* env_pos;
+    const float* env_rot;
+    float* out_distances;
+    int32_t* out_semantics;
+    int32_t* out_steps;                /* or NULL */
+    int32_t max_steps;
+    float max_distance;
+    float hit_epsilon;
+} navi_relaid_launch;
+
+/*
+ * navi_trace_relaid / navi_trace_relaid_poses with every argument in one
+ * struct (no reference counterpart), adding the leaf table for semantics of
+ * 0x7fff and above (the format's 16-bit field, docs/GMDAG.md:215,223).
+ */
+int navi_trace_relaid_ex(const navi_relaid_launch* launch, void* stream);
+
 /*
  * Launch shape of the record-layout tracer (no reference counterpart: a tuning
  * knob of this library). Launches of at least `n_rays` rays whose scenes'
@@ -253,6 +362,8 @@ typedef struct navi_point_queries {
     float* out_distances;              /* [n_points] */
     int32_t* out_semantics;            /* [n_points] */
     int32_t* out_kind;                 /* [n_points] or NULL */
+    const uint32_t* leaves;            /* the pool's leaf table (navi_relayout_leaves), or NULL */
+    uint32_t n_leaves;                 /* its entries (0 for none) */
 } navi_point_queries;
 
 /*

@@ -74,6 +74,11 @@ _lib.navi_trace_relaid_poses.argtypes = [
     _vp, ctypes.c_uint64, _vp, ctypes.c_int32, _vp, ctypes.c_int32, _vp, _vp, ctypes.c_int64, ctypes.c_int64,
     ctypes.c_int32, _vp, _vp, _vp, _vp, _vp, ctypes.c_int32, ctypes.c_float, ctypes.c_float, _vp, _vp,
 ]
+_lib.navi_relayout_leaves.restype = ctypes.c_int
+_lib.navi_relayout_leaves.argtypes = [_vp, ctypes.c_uint64, _vp, ctypes.c_uint64, _u64p, _u32p, _vp, _vp,
+                                      ctypes.c_uint32, _u32p]
+_lib.navi_scene_flags.restype = ctypes.c_int
+_lib.navi_scene_flags.argtypes = [_vp, ctypes.c_uint64, ctypes.c_uint32, _vp, ctypes.c_uint32, _u32p]
 
 
 class PointQueries(ctypes.Structure):
@@ -82,7 +87,39 @@ class PointQueries(ctypes.Structure):
     _fields_ = [("records", _vp), ("n_records", ctypes.c_uint64), ("scenes", _vp), ("n_scenes", ctypes.c_int32),
                 ("cell_tables", _vp), ("table_depth", ctypes.c_int32), ("point_scene", _vp), ("points", _vp),
                 ("n_points", ctypes.c_int64),
-                ("out_distances", _vp), ("out_semantics", _vp), ("out_kind", _vp)]
+                ("out_distances", _vp), ("out_semantics", _vp), ("out_kind", _vp),
+                ("leaves", _vp), ("n_leaves", ctypes.c_uint32)]
+
+
+class RelaidLaunch(ctypes.Structure):
+    """navi_relaid_launch (include/navi_trace.h)."""
+
+    _fields_ = [("records", _vp), ("n_records", ctypes.c_uint64), ("leaves", _vp), ("n_leaves", ctypes.c_uint32),
+                ("scenes", _vp), ("n_scenes", ctypes.c_int32), ("cell_tables", _vp), ("table_depth", ctypes.c_int32),
+                ("env_scene", _vp), ("env_order", _vp), ("n_envs", ctypes.c_int64), ("rays_per_env", ctypes.c_int64),
+                ("elevation_bins", ctypes.c_int32), ("origins", _vp), ("dirs", _vp), ("local_dirs", _vp),
+                ("env_pos", _vp), ("env_rot", _vp), ("out_distances", _vp), ("out_semantics", _vp),
+                ("out_steps", _vp), ("max_steps", ctypes.c_int32), ("max_distance", ctypes.c_float),
+                ("hit_epsilon", ctypes.c_float)]
+
+
+class LaunchInfo(ctypes.Structure):
+    """navi_launch_info (include/navi_trace.h)."""
+
+    _fields_ = [("kernels", ctypes.c_uint32), ("queue", ctypes.c_uint32), ("pair", ctypes.c_int32),
+                ("fast_planes", ctypes.c_uint32), ("planes", ctypes.c_uint32), ("staged", ctypes.c_uint32),
+                ("waves", ctypes.c_uint32), ("n_rays", ctypes.c_uint64)]
+
+
+_lib.navi_trace_relaid_ex.restype = ctypes.c_int
+_lib.navi_trace_relaid_ex.argtypes = [ctypes.POINTER(RelaidLaunch), _vp]
+_lib.navi_last_launch.restype = ctypes.c_int
+_lib.navi_last_launch.argtypes = [ctypes.POINTER(LaunchInfo)]
+
+# navi_launch_info bits and kinds (include/navi_trace.h)
+KERNEL_FAST, KERNEL_FAST_WIDE, KERNEL_COMBINED, KERNEL_RAW = 1, 2, 4, 8
+QUEUE_NONE, QUEUE_STREAM, QUEUE_CAPTURE, QUEUE_LEASE, QUEUE_SCRATCH = 0, 1, 2, 3, 4
+QUEUE_NAMES = {0: "none", 1: "stream", 2: "capture", 3: "lease", 4: "scratch"}
 
 
 class Observation(ctypes.Structure):
@@ -108,15 +145,79 @@ RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot",
 SCENE_NONNEG_LEAVES = 1  # navi_relaid_scene.flags bit (include/navi_trace.h)
 
 
-def nonneg_leaves(records, root_slot) -> bool:
-    """Whether no leaf slot of ``records`` (uint32 [n, 8]) nor an inlined root leaf has
-    its fp16 sign bit set (``NAVI_SCENE_NONNEG_LEAVES``)."""
+def scene_flags(records, root_slot, leaves=None) -> int:
+    """``navi_scene_flags``: the NAVI_SCENE_* bits the records reachable from
+    ``root_slot`` support (``records`` uint32 [n, 8] as navi_build_cell_table takes them,
+    ``leaves`` the pool's leaf table or None)."""
     import numpy as np
 
-    rec = np.asarray(records, dtype=np.uint32)
-    leaf_neg = (rec >> np.uint32(31)).astype(bool) & ((rec >> np.uint32(15)) & np.uint32(1)).astype(bool)
+    rec = np.ascontiguousarray(records, dtype=np.uint32).reshape(-1, 8)
+    lv = np.ascontiguousarray(leaves if leaves is not None else np.zeros(0, np.uint32), dtype=np.uint32)
+    out = ctypes.c_uint32()
+    check(_lib.navi_scene_flags(rec.ctypes.data if rec.size else None, rec.shape[0], int(root_slot),
+                                lv.ctypes.data if lv.size else None, lv.size, ctypes.byref(out)))
+    return int(out.value)
+
+
+def nonneg_leaves(records, root_slot, leaves=None) -> bool:
+    """Whether no reachable leaf has its fp16 sign bit set (``NAVI_SCENE_NONNEG_LEAVES``)."""
+    return bool(scene_flags(records, root_slot, leaves) & SCENE_NONNEG_LEAVES)
+
+
+def last_launch() -> dict:
+    """``navi_last_launch``: what the calling thread's last tracer launch enqueued."""
+    info = LaunchInfo()
+    check(_lib.navi_last_launch(ctypes.byref(info)))
+    k = info.kernels
+    return {"fast": bool(k & KERNEL_FAST), "fast_wide": bool(k & KERNEL_FAST_WIDE),
+            "combined": bool(k & KERNEL_COMBINED), "raw": bool(k & KERNEL_RAW),
+            "queue": QUEUE_NAMES.get(info.queue, str(info.queue)), "pair": info.pair,
+            "fast_planes": info.fast_planes, "planes": info.planes, "staged": bool(info.staged),
+            "waves": info.waves, "n_rays": info.n_rays}
+
+
+def relayout_leaves(words):
+    """``navi_relayout_leaves``: ``(records uint32 [n, 8], root_slot, levels_prefix[8],
+    leaves uint32 [m])``; leaves of semantic 0x7fff or above go to the leaf table (slot
+    0xffff0000 | entry). Raises RuntimeError (NAVI_E_LAYOUT) beyond 65536 entries."""
+    import numpy as np
+
+    w = np.ascontiguousarray(np.asarray(words).view(np.uint64).reshape(-1))
+    n = ctypes.c_uint64()
+    root = ctypes.c_uint32()
+    n_leaves = ctypes.c_uint32()
+    levels = np.zeros(8, np.uint64)
+    check(_lib.navi_relayout_leaves(w.ctypes.data, w.size, None, 0, ctypes.byref(n), ctypes.byref(root),
+                                    levels.ctypes.data, None, 0, ctypes.byref(n_leaves)))
+    rec = np.zeros((max(1, n.value), 8), np.uint32)
+    leaves = np.zeros(max(1, n_leaves.value), np.uint32)
+    check(_lib.navi_relayout_leaves(w.ctypes.data, w.size, rec.ctypes.data, n.value, ctypes.byref(n),
+                                    ctypes.byref(root), levels.ctypes.data, leaves.ctypes.data, leaves.size,
+                                    ctypes.byref(n_leaves)))
+    return rec[: n.value], int(root.value), levels, leaves[: n_leaves.value]
+
+
+TABLE_LEAF = 0xFFFF0000  # a leaf slot of the leaf table; the low 16 bits index it
+
+
+def rebase_leaves(records, root_slot, offset):
+    """Records and root slot with every leaf-table slot's entry moved by ``offset`` (a
+    scene's place in a pool's concatenated leaf table)."""
+    import numpy as np
+
+    rec = np.asarray(records, np.uint32).copy()
+    table = (rec & np.uint32(TABLE_LEAF)) == np.uint32(TABLE_LEAF)
+    if offset and table.any():
+        idx = (rec[table] & np.uint32(0xFFFF)) + np.uint32(offset)
+        if int(idx.max()) > 0xFFFF:
+            raise RuntimeError("leaf table of the pool exceeds 65536 entries")
+        rec[table] = np.uint32(TABLE_LEAF) | idx
     root = int(root_slot)
-    return not bool(leaf_neg.any()) and not (root >> 31 and (root >> 15) & 1)
+    if offset and (root & TABLE_LEAF) == TABLE_LEAF:
+        if (root & 0xFFFF) + offset > 0xFFFF:
+            raise RuntimeError("leaf table of the pool exceeds 65536 entries")
+        root = TABLE_LEAF | ((root & 0xFFFF) + offset)
+    return rec, root
 
 
 def relayout(words):

@@ -163,6 +163,8 @@ __global__ __launch_bounds__(256) void trace_raw_kernel(
 
 namespace navi {
 
+extern thread_local navi_launch_info g_last_launch;  // trace_relaid.hip
+
 int launch_raw(const uint64_t* pool, uint64_t n_words, Box dom, const navi_scene_desc* scenes,
                int32_t n_scenes, const int32_t* env_scene, int64_t rays_per_env, const float* origins,
                const float* dirs, float* out_d, int32_t* out_s, int32_t* out_steps, uint32_t* out_words,
@@ -170,6 +172,11 @@ int launch_raw(const uint64_t* pool, uint64_t n_words, Box dom, const navi_scene
     const int threads = 256;
     const int64_t blocks = (n_rays + threads - 1) / threads;
     if (blocks > 0x7fffffff) return set_error(NAVI_E_ARG, "too many rays for one launch");
+    g_last_launch = navi_launch_info{};
+    g_last_launch.kernels = NAVI_KERNEL_RAW;
+    g_last_launch.pair = -1;
+    g_last_launch.n_rays = static_cast<uint64_t>(n_rays);
+    g_last_launch.waves = static_cast<uint32_t>(blocks * (threads / 64));
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid(static_cast<unsigned>(blocks)), block(threads);
     const bool multi = scenes != nullptr;

@@ -66,6 +66,8 @@ struct PostParams {
     int32_t* __restrict__ point_s;
     int32_t* __restrict__ point_kind;  // or null
     int32_t point_blocks;              // workgroups answering point queries; the rest do envs
+    const uint32_t* __restrict__ leaves;  // leaf table (slots 0xffff0000 | i), or null
+    uint32_t n_leaves;
 };
 
 // kernel.cu:88-200 from the root at one point, no caches. Outside the domain:
@@ -113,8 +115,13 @@ __device__ void point_query(const PostParams& P, int32_t i) {
             }
             if (slot & 0x80000000u) {
                 if (depth < kMaxDepth) {
-                    d = half_to_float(slot & 0xffffu);
-                    s = static_cast<int32_t>((slot >> 16) & 0x7fffu);
+                    // an inline leaf (15-bit semantic), or a leaf-table entry (16-bit;
+                    // 0 past the table's end)
+                    uint32_t w = slot & 0x7fffffffu;
+                    if ((slot & 0xffff0000u) == 0xffff0000u)
+                        w = (P.leaves != nullptr && (slot & 0xffffu) < P.n_leaves) ? P.leaves[slot & 0xffffu] : 0u;
+                    d = half_to_float(w & 0xffffu);
+                    s = static_cast<int32_t>(w >> 16);
                     kind = kKindLeaf;
                 } else {
                     kind = kKindDepth;
@@ -383,6 +390,9 @@ int points_setup(PostParams& P, const navi_point_queries* Q) {
     P.point_d = Q->out_distances;
     P.point_s = Q->out_semantics;
     P.point_kind = Q->out_kind;
+    if (Q->n_leaves > 0 && !Q->leaves) return set_error(NAVI_E_ARG, "leaves must be non-null when n_leaves > 0");
+    P.leaves = Q->n_leaves > 0 ? Q->leaves : nullptr;
+    P.n_leaves = Q->n_leaves;
     return NAVI_OK;
 }
 

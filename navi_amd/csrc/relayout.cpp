@@ -17,18 +17,25 @@
 //   0x7ffffffd             the child index lies past the array: the reference
 //                          reads out of range when it examines the child
 //                          (only below the 32-level limit of kernel.cu:136)
-//   bit 31 set             leaf inlined: bits 30..16 semantic, 15..0 fp16 distance
+//   0xffff0000 | i         leaf whose semantic is 0x7fff or above (the format's
+//                          field is 16 bits, docs/GMDAG.md:215,223): entry i of
+//                          a leaf table of u32 (semantic << 16) | fp16 distance
+//   bit 31 set             leaf inlined: bits 30..16 semantic (below 0x7fff),
+//                          15..0 fp16 distance
 //   otherwise              index of the child's record
 // Descending one level is one 4-byte load at record*8 + octant, and a leaf
-// costs no load of its own. Traversal semantics are unchanged: the tracer's
-// caches key on boxes, which depend only on the tree shape.
+// costs no load of its own (one more for a table leaf). Traversal semantics
+// are unchanged: the tracer's caches key on boxes, which depend only on the
+// tree shape.
 //
-// Not representable (NAVI_E_LAYOUT; use the reference-layout kernel): a leaf
-// reachable from the root with semantic > 0x7fff, or more than 0x7ffffffc
-// internal nodes.
+// Not representable (NAVI_E_LAYOUT; use the reference-layout kernel): more
+// than 0x7ffffffc internal nodes, more than 65536 distinct (semantic,
+// distance) pairs of semantic 0x7fff or above, or any such leaf when the
+// caller gives no leaf table (navi_relayout).
 #include <stdint.h>
 
 #include <cstring>
+#include <unordered_map>
 #include <vector>
 
 #include "navi_trace.h"
@@ -43,21 +50,47 @@ constexpr uint32_t kSlotVoid = 0x7fffffffu;
 constexpr uint32_t kSlotFault = 0x7ffffffeu;
 constexpr uint32_t kSlotBadChild = 0x7ffffffdu;  // lowest terminal slot value
 constexpr uint32_t kUnassigned = 0xffffffffu;
+constexpr uint32_t kTableLeaf = 0xffff0000u;  // a leaf slot whose semantic field is all ones
+constexpr uint32_t kMaxTableLeaves = 0x10000u;
+
+// The leaf table being built: distinct (semantic << 16 | distance) words of
+// semantic 0x7fff or above, in order of first sight; null when the caller
+// gives none.
+struct LeafTable {
+    std::vector<uint32_t> words;
+    std::unordered_map<uint32_t, uint32_t> index;
+};
+
+// Slot value of a leaf word (bit 63 set), or false when it needs a leaf table
+// that is absent or full.
+inline bool leaf_slot(uint64_t node, LeafTable* leaves, uint32_t& out) {
+    const uint32_t sem = static_cast<uint32_t>(node >> 16) & 0xffffu;
+    const uint32_t dist = static_cast<uint32_t>(node & 0xffffu);
+    if (sem < 0x7fffu) {
+        out = 0x80000000u | (sem << 16) | dist;
+        return true;
+    }
+    if (leaves == nullptr) return false;
+    const uint32_t word = (sem << 16) | dist;
+    auto it = leaves->index.find(word);
+    if (it == leaves->index.end()) {
+        if (leaves->words.size() >= kMaxTableLeaves) return false;
+        it = leaves->index.emplace(word, static_cast<uint32_t>(leaves->words.size())).first;
+        leaves->words.push_back(word);
+    }
+    out = kTableLeaf | it->second;
+    return true;
+}
 
 // Slot value for a child word index, assigning record ids on first sight.
 inline bool child_slot(const uint64_t* w, uint64_t n, uint32_t idx, std::vector<uint32_t>& rec_of,
-                       std::vector<uint32_t>& queue, uint32_t& out) {
+                       std::vector<uint32_t>& queue, LeafTable* leaves, uint32_t& out) {
     if (static_cast<uint64_t>(idx) >= n) {
         out = kSlotBadChild;
         return true;
     }
     const uint64_t node = w[idx];
-    if (node >> 63) {
-        const uint32_t sem = static_cast<uint32_t>(node >> 16) & 0xffffu;
-        if (sem > 0x7fffu) return false;
-        out = 0x80000000u | (sem << 16) | static_cast<uint32_t>(node & 0xffffu);
-        return true;
-    }
+    if (node >> 63) return leaf_slot(node, leaves, out);
     if (rec_of[idx] == kUnassigned) {
         if (queue.size() >= kSlotBadChild) return false;
         rec_of[idx] = static_cast<uint32_t>(queue.size());
@@ -115,17 +148,18 @@ uint32_t longest_chain(const uint32_t* records, uint64_t n_records, uint32_t roo
 
 }  // namespace
 
-extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records,
-                             uint64_t cap_records, uint64_t* n_records, uint32_t* root_slot,
-                             uint64_t* n_levels_prefix) {
+namespace {
+
+int relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records, uint64_t cap_records,
+             uint64_t* n_records, uint32_t* root_slot, uint64_t* n_levels_prefix, LeafTable* leaves) {
     using navi::set_error;
     if (!words || n_words == 0) return set_error(NAVI_E_ARG, "dag must hold at least one word");
     if (!n_records || !root_slot) return set_error(NAVI_E_ARG, "n_records and root_slot are required");
     const uint64_t root = words[0];
     if (root >> 63) {  // a one-leaf DAG: no records
-        const uint32_t sem = static_cast<uint32_t>(root >> 16) & 0xffffu;
-        if (sem > 0x7fffu) return set_error(NAVI_E_LAYOUT, "leaf semantic %u exceeds 15 bits", sem);
-        *root_slot = 0x80000000u | (sem << 16) | static_cast<uint32_t>(root & 0xffffu);
+        if (!leaf_slot(root, leaves, *root_slot))
+            return set_error(NAVI_E_LAYOUT, "leaf semantic %u needs a leaf table",
+                             static_cast<uint32_t>(root >> 16) & 0xffffu);
         *n_records = 0;
         if (n_levels_prefix) std::memset(n_levels_prefix, 0, 8 * sizeof(uint64_t));
         return NAVI_OK;
@@ -163,9 +197,13 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
                 continue;
             }
             const uint32_t child = static_cast<uint32_t>(words[tab]);
-            if (!child_slot(words, n_words, child, rec_of, queue, slots[oct]))
-                return set_error(NAVI_E_LAYOUT, "DAG not representable in the device layout "
-                                                "(leaf semantic above 0x7fff or too many nodes)");
+            if (!child_slot(words, n_words, child, rec_of, queue, leaves, slots[oct]))
+                return set_error(NAVI_E_LAYOUT, leaves ? "DAG not representable in the device layout (more than "
+                                                         "65536 distinct leaves of semantic 0x7fff or above, or "
+                                                         "too many nodes)"
+                                                       : "DAG not representable in the device layout (a leaf "
+                                                         "semantic of 0x7fff or above needs a leaf table, "
+                                                         "navi_relayout_leaves; or too many nodes)");
         }
         if (out_records) {
             if (r >= cap_records) return set_error(NAVI_E_ARG, "record buffer too small");
@@ -182,6 +220,74 @@ extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* 
         for (size_t k = 0; k < 8 * queue.size(); ++k)
             if (out_records[k] == kSlotBadChild) out_records[k] = kSlotFault;
     }
+    return NAVI_OK;
+}
+
+}  // namespace
+
+extern "C" int navi_relayout(const uint64_t* words, uint64_t n_words, uint32_t* out_records,
+                             uint64_t cap_records, uint64_t* n_records, uint32_t* root_slot,
+                             uint64_t* n_levels_prefix) {
+    return relayout(words, n_words, out_records, cap_records, n_records, root_slot, n_levels_prefix, nullptr);
+}
+
+extern "C" int navi_relayout_leaves(const uint64_t* words, uint64_t n_words, uint32_t* out_records,
+                                    uint64_t cap_records, uint64_t* n_records, uint32_t* root_slot,
+                                    uint64_t* n_levels_prefix, uint32_t* out_leaves, uint32_t cap_leaves,
+                                    uint32_t* n_leaves) {
+    using navi::set_error;
+    if (!n_leaves) return set_error(NAVI_E_ARG, "n_leaves is required");
+    LeafTable leaves;
+    const int code = relayout(words, n_words, out_records, cap_records, n_records, root_slot, n_levels_prefix,
+                              &leaves);
+    if (code != NAVI_OK) return code;
+    *n_leaves = static_cast<uint32_t>(leaves.words.size());
+    if (out_leaves) {
+        if (leaves.words.size() > cap_leaves) return set_error(NAVI_E_ARG, "leaf table buffer too small");
+        if (!leaves.words.empty()) std::memcpy(out_leaves, leaves.words.data(), leaves.words.size() * 4);
+    }
+    return NAVI_OK;
+}
+
+// The NAVI_SCENE_* flags the records reachable from root_slot support: an
+// iterative walk over the internal records (each visited once; out-of-range
+// records end their branch) that looks at every leaf slot's fp16 sign bit,
+// in the leaf table for a table leaf.
+extern "C" int navi_scene_flags(const uint32_t* records, uint64_t n_records, uint32_t root_slot,
+                                const uint32_t* leaves, uint32_t n_leaves, uint32_t* flags) {
+    using navi::set_error;
+    if (!flags || (!records && n_records) || (!leaves && n_leaves)) return set_error(NAVI_E_ARG, "null argument");
+    bool negative = false;
+    auto leaf_negative = [&](uint32_t slot) {
+        uint32_t word = slot;
+        if ((slot & kTableLeaf) == kTableLeaf) {
+            const uint32_t i = slot & 0xffffu;
+            if (i >= n_leaves) return false;  // the tracer reads 0 there: distance +0
+            word = leaves[i];
+        }
+        return ((word >> 15) & 1u) != 0u;
+    };
+    if (root_slot & 0x80000000u) {
+        negative = leaf_negative(root_slot);
+    } else if (root_slot < n_records) {
+        std::vector<uint8_t> seen(n_records, 0);
+        std::vector<uint32_t> stack{root_slot};
+        seen[root_slot] = 1;
+        while (!stack.empty() && !negative) {
+            const uint32_t r = stack.back();
+            stack.pop_back();
+            for (uint32_t oct = 0; oct < 8u; ++oct) {
+                const uint32_t slot = records[8ull * r + oct];
+                if (slot & 0x80000000u) {
+                    negative = negative || leaf_negative(slot);
+                } else if (slot < kSlotBadChild && slot < n_records && !seen[slot]) {
+                    seen[slot] = 1;
+                    stack.push_back(slot);
+                }
+            }
+        }
+    }
+    *flags = negative ? 0u : NAVI_SCENE_NONNEG_LEAVES;
     return NAVI_OK;
 }
 

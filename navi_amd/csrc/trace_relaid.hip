@@ -53,6 +53,7 @@
 #include <thread>
 #include <unordered_map>
 #include <utility>
+#include <vector>
 
 #include "navi_trace.h"
 #include "trace_common.hpp"
@@ -134,7 +135,25 @@ struct RelaidParams {
     uint32_t small_tables;         // the cell tables span fewer than 2^32 bytes
     uint32_t stage;                // finished rays staged per tile in LDS (fast march)
     uint32_t after_fast;           // launched after trace_fast_kernel: return if that one ran
+    // leaf table of the leaves of semantic 0x7fff or above (slot 0xffff0000 | i
+    // holds entry i: semantic << 16 | fp16 distance), or null; sem_bits is 16
+    // with a table (the march then keeps leaf words without their slot bit),
+    // else 15 (the inline slot's field)
+    const uint32_t* __restrict__ leaves;
+    uint32_t n_leaves;
+    uint32_t sem_bits;
 };
+
+constexpr uint32_t kTableLeaf = 0xffff0000u;  // a leaf slot of the leaf table (low 16 bits: entry)
+
+// The leaf word of a leaf slot with its slot bit cleared: semantic in bits
+// 31..16 (16 bits), fp16 distance in 15..0; a table leaf's entry, 0 past the
+// table's end (distance +0, semantic 0).
+__device__ __forceinline__ uint32_t table_leaf_word(uint32_t slot, const uint32_t* leaves, uint32_t n_leaves) {
+    if ((slot & kTableLeaf) != kTableLeaf) return slot & 0x7fffffffu;
+    const uint32_t i = slot & 0xffffu;
+    return i < n_leaves ? leaves[i] : 0u;
+}
 
 // Work index q -> ray id (env * R + r).
 __device__ __forceinline__ uint32_t ray_of(const RelaidParams& P, uint32_t q, int32_t& env_out) {
@@ -483,7 +502,10 @@ __device__ __forceinline__ const RelaidParams& reload_params() {
 // leaf-run step (tame boxes) and the box faces behind the ray (below). The
 // step's conditions are wave masks, so its path has no short-circuit branches,
 // and the cell table is read through a buffer resource (32-bit offsets).
-template <int kDepth, int kPD, bool kPoses, bool kQueued>
+// kLeaves: the launch may have a leaf table (16-bit semantics), checked at run
+// time; false compiles the table's handling out (the fast kernel's instances
+// for launches without one: measured, the handling costs those 1.2%).
+template <int kDepth, int kPD, bool kPoses, bool kQueued, bool kLeaves>
 __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds* lds_scenes,
                                            const float* lds_planes, uint32_t* lds_stage) {
     static_assert(kPD >= 4 && kPD <= 8 && kDepth >= 4 && kDepth <= kPD + 2 && kDepth <= 7,
@@ -619,7 +641,9 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 lfx = root_leaf ? dmx : nan;
                 lfy = root_leaf ? dmy : nan;
                 lfz = root_leaf ? dmz : nan;
-                lf_slot = S.root;
+                lf_slot = (kLeaves && RP.leaves != nullptr && root_leaf)
+                              ? table_leaf_word(S.root, RP.leaves, RP.n_leaves)
+                              : S.root;
             }
             const uint64_t started = wave_mask(fresh);
             neg_x = wave_mask(__float_as_int(dx) < 0);
@@ -830,6 +854,10 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
         lfy = new_leaf ? hy : lfy;
         lfz = new_leaf ? hz : lfz;
         lf_slot = new_leaf ? slot : lf_slot;
+        if (kLeaves && P.leaves != nullptr) {  // uniform: the pool has a leaf table (16-bit semantics)
+            const RelaidParams& RP = reload_params();
+            if (new_leaf) lf_slot = table_leaf_word(slot, RP.leaves, RP.n_leaves);
+        }
 
         // ---- finish the step (kernel.cu:54-85, 297-308) ----
         // The exit quotient (face - p) / d of the reference's face (hi when
@@ -842,7 +870,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                               kOutsideDomain);
         const float void_d = e > kVoidAdvanceEps ? e : kVoidAdvanceEps;  // fmaxf: e is never NaN
         const float leaf_d = half_to_float(lf_slot & 0xffffu);
-        const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
+        const int32_t leaf_s =
+            static_cast<int32_t>(kLeaves ? __builtin_amdgcn_ubfe(lf_slot, 16u, P.sem_bits) : (lf_slot >> 16) & 0x7fffu);
         // the step's distance: the void's exit, the leaf's, the outside-domain
         // step, or NaN after a fault (so t becomes NaN); a ray's semantic is its
         // leaf's when the step hits and 0 whenever it ends otherwise, so only
@@ -985,7 +1014,7 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
                 const SceneLds& S = lds_scenes[scene];
                 if (S.root & 0x80000000u) {
                     lf = Box{S.x0, S.y0, S.z0, S.x1, S.y1, S.z1};
-                    lf_slot = S.root;
+                    lf_slot = RP.leaves != nullptr ? table_leaf_word(S.root, RP.leaves, RP.n_leaves) : S.root;
                     lf_ok = true;
                 }
             }
@@ -1256,6 +1285,10 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
         lf.y1 = new_leaf ? cur.y1 : lf.y1;
         lf.z1 = new_leaf ? cur.z1 : lf.z1;
         lf_slot = new_leaf ? slot : lf_slot;
+        if (P.leaves != nullptr) {  // uniform: the pool has a leaf table (16-bit semantics)
+            const RelaidParams& RP = reload_params();
+            if (new_leaf) lf_slot = table_leaf_word(slot, RP.leaves, RP.n_leaves);
+        }
         lf_ok = lf_ok || new_leaf;
 
         // ---- finish the step (kernel.cu:297-308) ----
@@ -1285,7 +1318,7 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
         }
         const float void_d = fmaxf(e, kVoidAdvanceEps);
         const float leaf_d = half_to_float(lf_slot & 0xffffu);
-        const int32_t leaf_s = static_cast<int32_t>((lf_slot >> 16) & 0x7fffu);
+        const int32_t leaf_s = static_cast<int32_t>(__builtin_amdgcn_ubfe(lf_slot, 16u, P.sem_bits));
         // stale (32 levels without leaf or void): dist / sem keep their values
         dist = is_void ? void_d : (is_leaf ? leaf_d : (outside ? kOutsideDomain : dist));
         sem = is_void ? 0 : (is_leaf ? leaf_s : (outside ? 0 : sem));
@@ -1416,7 +1449,7 @@ __device__ __forceinline__ void rearm_queue(const RelaidParams& P) {
 // fit one of its two shapes and the launch has a work queue; it records in the
 // queue's third word whether the fast march applied and returns at once when
 // it does not (the general kernel, launched next, then traces the launch).
-template <int kDepth, int kPD, bool kPoses, int kThreads>
+template <int kDepth, int kPD, bool kPoses, int kThreads, bool kLeaves>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void trace_fast_kernel(RelaidParams P) {
     static_assert(kPD >= 4 && kPD <= 8 && kDepth >= 4 && kDepth <= kPD + 2 && kDepth <= 7,
                   "planes of 4..8 levels, the table at most two levels below them");
@@ -1426,8 +1459,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) v
     const bool fast = fast_applies(P, c);
     if (blockIdx.x == 0 && threadIdx.x == 0) P.queue[2] = fast ? 1u : 0u;
     if (!fast) return;
-    march_fast<kDepth, kPD, kPoses, true>(P, lds_scenes, lds_planes,
-                                    reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
+    march_fast<kDepth, kPD, kPoses, true, kLeaves>(P, lds_scenes, lds_planes,
+                                             reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
     rearm_queue(P);
 }
 
@@ -1446,8 +1479,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void t
     const LaunchConds c = stage_scenes<kPD>(P, lds_scenes, lds_planes);
     if constexpr (kPlanes) {
         if (fast_applies(P, c))
-            march_fast<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes,
-                                            reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
+            march_fast<kDepth, kPD, kPoses, false, true>(
+                P, lds_scenes, lds_planes, reinterpret_cast<uint32_t*>(lds_planes + P.n_scenes * scene_stride(kPD)));
         else
             march<kDepth, kPD, kPoses, false>(P, lds_scenes, lds_planes, c.tame, c.shallow, c.planes, c.void_cache);
     } else {
@@ -1465,26 +1498,44 @@ std::map<std::pair<std::pair<int, int>, size_t>, int> g_grid_blocks;
 // Work-queue counters: [next unit, finished waves, the fast kernel traced the
 // launch, unused] in one 64 KiB device buffer per device, allocated and zeroed
 // by navi_device_init (the third word is written by each fast kernel before the
-// general kernel after it reads it; "pair" below means these four words). An eager launch
-// uses the pair of its (stream, thread for hipStreamPerThread): launches on one
-// stream run in order, so the pair is never used by two launches at once, and
-// the kernel's last wave rearms it for the next. A launch recorded into a graph
-// gets a pair of its own, never shared: a graph may be replayed on any stream,
-// and two launches of one capture may run concurrently; replays of one graph
-// run in order and each rearms the pair. Launches find no pair (and take the
-// static schedule) once kQueueSlots are in use, or while a stream captures on a
-// device that was never initialised (no allocation inside a capture).
+// general kernel after it reads it; "pair" below means these four words).
+// * An eager launch uses the pair of its (stream, thread for
+//   hipStreamPerThread): launches on one stream run in order, so the pair is
+//   never used by two launches at once, and the kernel's last wave rearms it
+//   for the next.
+// * A launch recorded into a graph gets a pair of its own (a graph may be
+//   replayed on any stream, and two launches of one capture may run at once),
+//   cleared by a small kernel node before the tracer on every replay. A HIP
+//   user object retained by the graph gives the pair back when the graph and
+//   the executable graphs made from it are destroyed.
+// * When the table's pairs are all taken, an eager launch leases one of the
+//   reserve pairs: one whose event (recorded after its last launch) has
+//   completed, cleared before the launch. A launch finds no pair (and takes the
+//   static schedule) only while every reserve pair is in flight, or while a
+//   stream captures on a device that was never initialised (no allocation
+//   inside a capture).
 constexpr int kQueueSlots = 4096;
 constexpr int kQueueWords = 4;
+constexpr int kLeasePairs = 64;                          // the table's last pairs
+constexpr int kTablePairs = kQueueSlots - kLeasePairs;  // streams and captures
 std::mutex g_queue_mu;
 struct DeviceQueues {
     uint32_t* mem = nullptr;
-    int used = 0;
-    std::map<std::pair<void*, size_t>, int> slot;  // (stream, thread) -> pair
+    int used = 0;                                    // table pairs handed out, [0, kTablePairs)
+    std::vector<int> free_pairs;                     // given back by destroyed graphs
+    std::map<std::pair<void*, size_t>, int> slot;   // (stream, thread) -> pair
+    hipEvent_t lease_event[kLeasePairs] = {};
+    uint8_t lease_busy[kLeasePairs] = {};            // 1: being set up by a launch (event not yet recorded)
+    uint8_t lease_used[kLeasePairs] = {};            // an event has been recorded after a launch
+    int lease_next = 0;
 };
 std::unordered_map<int, DeviceQueues> g_queues;
 
-// Allocates the current device's counters if it has none (g_queue_mu held).
+// The calling thread's last launch (navi_last_launch).
+thread_local navi_launch_info g_last_launch = {};
+
+// Allocates the current device's counters and lease events if it has none
+// (g_queue_mu held).
 int init_device_locked(int dev) {
     DeviceQueues& q = g_queues[dev];
     if (q.mem != nullptr) return NAVI_OK;
@@ -1496,28 +1547,115 @@ int init_device_locked(int dev) {
         (void)hipFree(p);
         return set_error(NAVI_E_LAUNCH, "work-queue counters: clearing failed on device %d", dev);
     }
+    for (int i = 0; i < kLeasePairs; ++i) {
+        if (hipEventCreateWithFlags(&q.lease_event[i], hipEventDisableTiming) != hipSuccess) {
+            for (int k = 0; k < i; ++k) (void)hipEventDestroy(q.lease_event[k]);
+            (void)hipFree(p);
+            return set_error(NAVI_E_LAUNCH, "work-queue counters: hipEventCreate failed on device %d", dev);
+        }
+    }
     q.mem = static_cast<uint32_t*>(p);
     return NAVI_OK;
 }
 
-uint32_t* queue_for(hipStream_t stream) {
+// A capture's pair, handed back by the destructor of the user object the
+// captured graph retains.
+struct CapturePair {
+    int dev, pair;
+};
+void release_capture_pair(void* p) {
+    CapturePair* cp = static_cast<CapturePair*>(p);
+    {
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        g_queues[cp->dev].free_pairs.push_back(cp->pair);
+    }
+    delete cp;
+}
+
+// The pair a launch on `stream` uses: its counter words (null for none), its
+// NAVI_QUEUE_* kind and table index; a leased pair's lease index in *lease.
+struct QueueChoice {
+    uint32_t* words = nullptr;
+    uint32_t kind = NAVI_QUEUE_NONE;
+    int pair = -1;
+    int lease = -1;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+};
+
+QueueChoice queue_for(hipStream_t stream) {
+    QueueChoice c;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return c;
+    c.dev = dev;
     hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &status) != hipSuccess) status = hipStreamCaptureStatusNone;
     const bool capturing = status != hipStreamCaptureStatusNone;
-    std::lock_guard<std::mutex> lock(g_queue_mu);
-    DeviceQueues& q = g_queues[dev];
-    if (q.mem == nullptr && (capturing || init_device_locked(dev) != NAVI_OK)) return nullptr;
-    if (capturing) return q.used < kQueueSlots ? q.mem + kQueueWords * q.used++ : nullptr;
-    const size_t thread = stream == hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
-    const auto key = std::make_pair(static_cast<void*>(stream), thread);
-    auto it = q.slot.find(key);
-    if (it == q.slot.end()) {
-        if (q.used >= kQueueSlots) return nullptr;
-        it = q.slot.emplace(key, q.used++).first;
+    {
+        std::lock_guard<std::mutex> lock(g_queue_mu);
+        DeviceQueues& q = g_queues[dev];
+        if (q.mem == nullptr && (capturing || init_device_locked(dev) != NAVI_OK)) return c;
+        if (capturing) {
+            if (!q.free_pairs.empty()) {
+                c.pair = q.free_pairs.back();
+                q.free_pairs.pop_back();
+            } else if (q.used < kTablePairs) {
+                c.pair = q.used++;
+            } else {
+                return c;
+            }
+            c.kind = NAVI_QUEUE_CAPTURE;
+        } else {
+            const size_t thread =
+                stream == hipStreamPerThread ? std::hash<std::thread::id>{}(std::this_thread::get_id()) : 0;
+            const auto key = std::make_pair(static_cast<void*>(stream), thread);
+            auto it = q.slot.find(key);
+            if (it == q.slot.end() && q.used < kTablePairs) it = q.slot.emplace(key, q.used++).first;
+            if (it != q.slot.end()) {
+                c.pair = it->second;
+                c.kind = NAVI_QUEUE_STREAM;
+            } else {
+                // lease a reserve pair whose last launch has completed
+                for (int k = 0; k < kLeasePairs && c.lease < 0; ++k) {
+                    const int i = (q.lease_next + k) % kLeasePairs;
+                    if (q.lease_busy[i]) continue;
+                    if (q.lease_used[i] && hipEventQuery(q.lease_event[i]) != hipSuccess) continue;
+                    c.lease = i;
+                }
+                if (c.lease < 0) return c;
+                q.lease_busy[c.lease] = 1;
+                q.lease_next = (c.lease + 1) % kLeasePairs;
+                c.pair = kTablePairs + c.lease;
+                c.kind = NAVI_QUEUE_LEASE;
+            }
+        }
+        c.words = q.mem + kQueueWords * c.pair;
     }
-    return q.mem + kQueueWords * it->second;
+    if (c.kind == NAVI_QUEUE_CAPTURE) {
+        // tie the pair to the graph being captured (outside the lock: HIP may
+        // run destructors, which take it); on failure the pair stays taken
+        hipGraph_t graph = nullptr;
+        unsigned long long id = 0;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        hipUserObject_t obj = nullptr;
+        CapturePair* cp = new CapturePair{dev, c.pair};
+        if (hipStreamGetCaptureInfo_v2(stream, &st, &id, &graph, nullptr, nullptr) == hipSuccess && graph != nullptr &&
+            hipUserObjectCreate(&obj, cp, release_capture_pair, 1, hipUserObjectNoDestructorSync) == hipSuccess) {
+            (void)hipGraphRetainUserObject(graph, obj, 1, hipGraphUserObjectMove);
+        } else {
+            delete cp;
+        }
+    }
+    return c;
+}
+
+// After a leased launch was enqueued: record its event (the pair is free again
+// once it completes).
+void finish_lease(const QueueChoice& c, hipStream_t stream) {
+    if (c.kind != NAVI_QUEUE_LEASE) return;
+    std::lock_guard<std::mutex> lock(g_queue_mu);
+    DeviceQueues& q = g_queues[c.dev];
+    q.lease_used[c.lease] = hipEventRecord(q.lease_event[c.lease], stream) == hipSuccess ? 1 : 0;
+    q.lease_busy[c.lease] = q.lease_used[c.lease] ? 0 : 1;  // a failed record keeps the pair out of use
 }
 
 // Scratch of navi_trace_relaid_noalloc: one set of work-queue counter words per device
@@ -1580,9 +1718,10 @@ int resident_blocks(void (*kernel)(RelaidParams), int variant, size_t lds, bool 
     return blocks;
 }
 
-// Sizes the work units and the grid of one persistent launch and enqueues it.
+// Sizes the work units and the grid of one persistent launch and enqueues it;
+// *waves receives the grid's waves.
 int enqueue_relaid(void (*kernel)(RelaidParams), RelaidParams P, int variant, size_t lds, bool keep,
-                   hipStream_t stream, int threads = 256) {
+                   hipStream_t stream, int threads = 256, uint32_t* waves = nullptr) {
     const int grid_blocks = resident_blocks(kernel, variant, lds, keep, threads);
     const int waves_per_block = threads / 64;
     // Small batches: one-tile units, so that more waves get work (a launch
@@ -1594,6 +1733,7 @@ int enqueue_relaid(void (*kernel)(RelaidParams), RelaidParams P, int variant, si
     int64_t blocks = (static_cast<int64_t>(P.n_chunks) + waves_per_block - 1) / waves_per_block;
     if (blocks > grid_blocks) blocks = grid_blocks;
     if (blocks < 1) blocks = 1;
+    if (waves) *waves = static_cast<uint32_t>(blocks) * static_cast<uint32_t>(waves_per_block);
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(threads), lds, stream, P);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return set_error(NAVI_E_LAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
@@ -1622,14 +1762,39 @@ int plane_depth_wide(int32_t n_scenes, uint32_t D, size_t budget) {
 // range below the outside-domain distance and small tables) enqueues trace_fast_kernel, then
 // trace_relaid_kernel with after_fast, which returns at once when the fast
 // kernel traced it (every other launch: trace_relaid_kernel alone).
+int launch_relaid_queued(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue, navi_launch_info& info);
+
 int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = nullptr) {
-    const bool no_alloc = scratch_queue != nullptr;
+    navi_launch_info info = {};
+    info.n_rays = P.n_rays;
+    QueueChoice c;
+    if (scratch_queue != nullptr) {
+        c.words = scratch_queue;
+        c.kind = NAVI_QUEUE_SCRATCH;
+    } else {
+        c = queue_for(stream);
+    }
+    info.queue = c.kind;
+    info.pair = c.pair;
+    const int code = launch_relaid_queued(P, stream, c.words, info);
+    finish_lease(c, stream);  // also after a failed launch: the lease's event then completes at once
+    g_last_launch = info;
+    return code;
+}
+
+// The launch with its counter words `queue` (null: static schedule).
+int launch_relaid_queued(RelaidParams P, hipStream_t stream, uint32_t* queue, navi_launch_info& info) {
+    const bool no_alloc = info.queue == NAVI_QUEUE_SCRATCH;
     P.n_chunks = (P.n_rays + 63u) / 64u;
-    P.queue = no_alloc ? scratch_queue : queue_for(stream);
+    P.queue = queue;
     const uint32_t D = P.cell_depth;
     P.small_tables = (static_cast<uint64_t>(P.n_scenes) << (3u * D + 3u)) < (1ull << 32) ? 1u : 0u;
     const bool poses = P.local_dirs != nullptr;
-    if (no_alloc) hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
+    const bool leaves = P.leaves != nullptr;
+    // counters another launch may have used: cleared first (a kernel node,
+    // never a memset node, so the launch can be captured into a graph)
+    if (P.queue != nullptr && info.queue != NAVI_QUEUE_STREAM)
+        hipLaunchKernelGGL(clear_queue_kernel, dim3(1), dim3(64), 0, stream, P.queue);
 
     // the fast kernel: for large launches planes up to two levels below the
     // table in two 1024-thread workgroups per CU, else planes that fit eight
@@ -1647,8 +1812,10 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
             lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pw) * sizeof(float));
             F.stage = (F.out_steps == nullptr && lds + stage_lds(kWideThreads) <= kFastLdsWide) ? 1u : 0u;
             if (F.stage) lds += stage_lds(kWideThreads);
-#define NAVI_FAST(d, p) \
-    (poses ? trace_fast_kernel<d, p, true, kWideThreads> : trace_fast_kernel<d, p, false, kWideThreads>)
+#define NAVI_FAST(d, p)                                                                                       \
+    (leaves ? (poses ? trace_fast_kernel<d, p, true, kWideThreads, true> : trace_fast_kernel<d, p, false, kWideThreads, true>) \
+            : (poses ? trace_fast_kernel<d, p, true, kWideThreads, false>                                        \
+                     : trace_fast_kernel<d, p, false, kWideThreads, false>))
             switch (pw * 8 + static_cast<int>(D)) {
                 case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
                 case 5 * 8 + 4: fast = NAVI_FAST(4, 5); break;
@@ -1669,15 +1836,17 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
                 default: break;
             }
 #undef NAVI_FAST
-            variant = 2 * (pw * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 2048;
+            variant = 2 * (pw * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 2048 + (leaves ? 4096 : 0);
         }
-        const int pf = (fast == nullptr && F.n_rays >= kFastMinRays) ? plane_depth_for(F.n_scenes, D, kFastLds) : 0;
+        // (the 256-thread shape has no instances for leaf tables: such launches take the combined kernel)
+        const int pf = (fast == nullptr && !leaves && F.n_rays >= kFastMinRays) ? plane_depth_for(F.n_scenes, D, kFastLds)
+                                                                                : 0;
         if (pf != 0) {
             threads = 256;
             lds = static_cast<size_t>(F.n_scenes) * (sizeof(SceneLds) + scene_stride(pf) * sizeof(float));
             F.stage = (F.out_steps == nullptr && lds + kStageLds <= kFastLds) ? 1u : 0u;
             if (F.stage) lds += kStageLds;
-#define NAVI_FAST(d, p) (poses ? trace_fast_kernel<d, p, true, 256> : trace_fast_kernel<d, p, false, 256>)
+#define NAVI_FAST(d, p) (poses ? trace_fast_kernel<d, p, true, 256, false> : trace_fast_kernel<d, p, false, 256, false>)
             switch (pf * 8 + static_cast<int>(D)) {
                 case 4 * 8 + 4: fast = NAVI_FAST(4, 4); break;
                 case 4 * 8 + 5: fast = NAVI_FAST(5, 4); break;
@@ -1693,9 +1862,12 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
             variant = 2 * (pf * 8 + static_cast<int>(D)) + static_cast<int>(poses) + 1024;
         }
         if (fast != nullptr) {
-            const int code = enqueue_relaid(fast, F, variant, lds, !no_alloc, stream, threads);
+            const int code = enqueue_relaid(fast, F, variant, lds, !no_alloc, stream, threads, &info.waves);
             if (code != NAVI_OK) return code;
             P.after_fast = 1u;
+            info.kernels |= NAVI_KERNEL_FAST | (threads == kWideThreads ? NAVI_KERNEL_FAST_WIDE : 0u);
+            info.fast_planes = static_cast<uint32_t>(pw != 0 ? pw : pf);
+            info.staged = F.stage;
         }
     }
 
@@ -1722,8 +1894,11 @@ int launch_relaid(RelaidParams P, hipStream_t stream, uint32_t* scratch_queue = 
         default: kernel = NAVI_RELAID(0, 0); break;
     }
 #undef NAVI_RELAID
+    info.kernels |= NAVI_KERNEL_COMBINED;
+    info.planes = static_cast<uint32_t>(pd);
+    if (!P.after_fast) info.staged = P.stage;
     return enqueue_relaid(kernel, P, 2 * (pd * 8 + static_cast<int>(D)) + static_cast<int>(poses), lds, !no_alloc,
-                          stream);
+                          stream, 256, P.after_fast ? nullptr : &info.waves);
 }
 
 }  // namespace navi
@@ -1777,6 +1952,7 @@ int relaid_setup(RelaidParams& P, const uint32_t* records, uint64_t n_records, c
     P.max_steps = max_steps;
     P.max_distance = max_distance;
     P.hit_eps = hit_epsilon;
+    P.sem_bits = 15u;
     return NAVI_OK;
 }
 
@@ -1795,6 +1971,42 @@ extern "C" int navi_device_init(void) {
 }
 
 extern "C" uint64_t navi_set_wide_min_rays(uint64_t n_rays) { return navi::g_wide_min_rays.exchange(n_rays); }
+
+extern "C" int navi_last_launch(navi_launch_info* info) {
+    if (!info) return navi::set_error(NAVI_E_ARG, "info must be non-null");
+    *info = navi::g_last_launch;
+    return NAVI_OK;
+}
+
+extern "C" int navi_trace_relaid_ex(const navi_relaid_launch* L, void* stream) {
+    using namespace navi;
+    if (!L) return set_error(NAVI_E_ARG, "launch must be non-null");
+    RelaidParams P;
+    const int code = relaid_setup(P, L->records, L->n_records, L->scenes, L->n_scenes, L->cell_tables, L->table_depth,
+                                  L->env_scene, L->env_order, L->n_envs, L->rays_per_env, L->elevation_bins,
+                                  L->out_distances, L->out_semantics, L->max_steps, L->max_distance,
+                                  L->hit_epsilon, L->out_steps);
+    if (code != NAVI_OK || P.n_rays == 0) return code;
+    if (L->local_dirs) {
+        if (!L->env_pos || !L->env_rot) return set_error(NAVI_E_ARG, "env_pos and env_rot must be non-null");
+        P.local_dirs = L->local_dirs;
+        P.env_pos = L->env_pos;
+        P.env_rot = L->env_rot;
+    } else {
+        if (!L->origins || !L->dirs) return set_error(NAVI_E_ARG, "origins and dirs (or local_dirs) must be non-null");
+        P.origins = L->origins;
+        P.dirs = L->dirs;
+    }
+    if (L->n_leaves > 0) {
+        if (!L->leaves) return set_error(NAVI_E_ARG, "leaves must be non-null when n_leaves > 0");
+        if (L->n_leaves > 0x10000u) return set_error(NAVI_E_ARG, "a leaf table holds at most 65536 entries");
+        P.leaves = L->leaves;
+        P.n_leaves = L->n_leaves;
+        P.sem_bits = 16u;
+    }
+    return launch_relaid(P, static_cast<hipStream_t>(stream));
+}
+
 
 extern "C" int navi_trace_relaid_noalloc(const uint32_t* records, uint64_t n_records,
                                          const navi_relaid_scene* scenes, int32_t n_scenes,

@@ -126,17 +126,23 @@ class ResidentScenes:
         self.pool = torch.from_numpy(np.concatenate(chunks).view(np.int64)).to(self.device) if keep_words else None
         self.table = torch.from_numpy(table.view(np.uint8).copy()).to(self.device)
 
-        # device record layout (one 32-byte record per internal node)
+        # device record layout (one 32-byte record per internal node); leaves of
+        # semantic 0x7fff or above go to one leaf table shared by the pool
         rtable = np.zeros(len(scenes), dtype=_native.RELAID_SCENE_DTYPE)
         recs = []
+        leaf_tables = []
         roff = 0
+        loff = 0
         self.relaid_ok = True
         for i, w in enumerate(chunks):
             try:
-                rec, root, _levels = _native.relayout(w)
+                rec, root, _levels, leaves = _native.relayout_leaves(w)
+                rec, root = _native.rebase_leaves(rec, root, loff)
             except RuntimeError:
                 self.relaid_ok = False
                 break
+            leaf_tables.append(leaves)
+            loff += int(leaves.size)
             rtable[i]["rec_offset"] = roff
             rtable[i]["n_records"] = rec.shape[0]
             # child record slots become absolute pool indices
@@ -153,12 +159,17 @@ class ResidentScenes:
             # 32-bit byte size must not wrap: fewer than 2^27 records
             if roff >= (1 << 27):
                 self.relaid_ok = False
+        self.n_leaves = 0
+        self.leaves = None
         if self.relaid_ok:
             allrec = np.concatenate(recs) if roff else np.zeros((1, 8), np.uint32)
+            all_leaves = np.concatenate(leaf_tables) if loff else np.zeros(0, np.uint32)
             for i in range(len(scenes)):
                 rtable[i]["max_depth"] = _native.record_depth(allrec[:roff], int(rtable[i]["root_slot"]))
-                if _native.nonneg_leaves(recs[i], rtable[i]["root_slot"]):
-                    rtable[i]["flags"] |= _native.SCENE_NONNEG_LEAVES
+                rtable[i]["flags"] = _native.scene_flags(allrec[:roff], int(rtable[i]["root_slot"]), all_leaves)
+            if loff:
+                self.n_leaves = loff
+                self.leaves = torch.from_numpy(all_leaves.view(np.int32).copy()).to(self.device)
             if table_depth is not None:
                 self.table_depth = int(table_depth)
             else:
@@ -312,17 +323,10 @@ class ResidentScenes:
             self._poll_cost()
             order = self.env_order(env_scene) if sort_by_scene else None
             out_steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
-            with torch.cuda.device(self.device):
-                stream = torch.cuda.current_stream(self.device).cuda_stream
-                code = _native.lib().navi_trace_relaid(
-                    self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                    self.cell_tables.data_ptr(), self.table_depth,
-                    env_scene.data_ptr(), order.data_ptr() if order is not None else None, e, r,
-                    int(elevation_bins or 0), origins.data_ptr(), dirs.data_ptr(),
-                    out_distances.data_ptr(), out_semantics.data_ptr(), int(max_steps),
-                    float(max_distance), float(hit_epsilon),
-                    out_steps.data_ptr() if out_steps is not None else None, stream)
-            _native.check(code)
+            L = self._launch_args(env_scene.data_ptr(), order, e, r, elevation_bins, out_distances.data_ptr(),
+                                  out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon)
+            L.origins, L.dirs = origins.data_ptr(), dirs.data_ptr()
+            self._launch(L, e, r, elevation_bins, order)
             if measure:
                 self._start_cost_readback(out_steps, env_scene)
             return
@@ -351,7 +355,7 @@ class ResidentScenes:
         self._require_gpu()
         if not self.relaid_ok:
             raise RuntimeError("these scenes do not fit the device record layout "
-                               "(leaf semantic above 0x7fff or more than 2^27 records)")
+                               "(more than 65536 distinct leaves of semantic 0x7fff or above, or 2^27 records)")
 
     def _check(self, name: str, t: Any, dtype: Any, shape: tuple[int, ...], optional: bool = False) -> int | None:
         if t is None:
@@ -384,18 +388,37 @@ class ResidentScenes:
         self._poll_cost()
         order = self.env_order(env_scene) if sort_by_scene else None
         steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
-        ptrs[6] = steps.data_ptr() if steps is not None else None
-        with torch.cuda.device(self.device):
-            stream = torch.cuda.current_stream(self.device).cuda_stream
-            code = _native.lib().navi_trace_relaid_poses(
-                self.records.data_ptr(), self.n_records, self.relaid_table.data_ptr(), self.n_scenes,
-                self.cell_tables.data_ptr(), self.table_depth, ptrs[0],
-                order.data_ptr() if order is not None else None, e, r,
-                int(elevation_bins or 0), ptrs[1], ptrs[2], ptrs[3], ptrs[4], ptrs[5], int(max_steps),
-                float(max_distance), float(hit_epsilon), ptrs[6], stream)
-        _native.check(code)
+        L = self._launch_args(ptrs[0], order, e, r, elevation_bins, ptrs[4], ptrs[5], steps, max_steps,
+                              max_distance, hit_epsilon)
+        L.local_dirs, L.env_pos, L.env_rot = ptrs[1], ptrs[2], ptrs[3]
+        self._launch(L, e, r, elevation_bins, order)
         if measure:
             self._start_cost_readback(steps, env_scene)
+
+    # ---- launches ----
+
+    def _launch_args(self, env_scene_ptr, order, e, r, elevation_bins, out_d_ptr, out_s_ptr, steps, max_steps,
+                     max_distance, hit_epsilon) -> Any:
+        L = _native.RelaidLaunch()
+        L.records, L.n_records = self.records.data_ptr(), self.n_records
+        if self.n_leaves:
+            L.leaves, L.n_leaves = self.leaves.data_ptr(), self.n_leaves
+        L.scenes, L.n_scenes = self.relaid_table.data_ptr(), self.n_scenes
+        L.cell_tables, L.table_depth = self.cell_tables.data_ptr(), self.table_depth
+        L.env_scene = env_scene_ptr
+        L.env_order = order.data_ptr() if order is not None else None
+        L.n_envs, L.rays_per_env, L.elevation_bins = e, r, int(elevation_bins or 0)
+        L.out_distances, L.out_semantics = out_d_ptr, out_s_ptr
+        L.out_steps = steps.data_ptr() if steps is not None else None
+        L.max_steps, L.max_distance, L.hit_epsilon = int(max_steps), float(max_distance), float(hit_epsilon)
+        return L
+
+    def _launch(self, L, e: int, r: int, elevation_bins, order) -> None:
+        """Enqueues ``navi_trace_relaid_ex`` on the current stream."""
+        with torch.cuda.device(self.device):
+            stream = torch.cuda.current_stream(self.device).cuda_stream
+            code = _native.lib().navi_trace_relaid_ex(ctypes.byref(L), stream)
+        _native.check(code)
 
     def _point_queries(self, points, out_distances, out_semantics, point_scene, out_kind, prefix=""):
         self._require_relaid()
@@ -410,6 +433,8 @@ class ResidentScenes:
         q.out_distances = self._check(prefix + "distances", out_distances, torch.float32, (p,))
         q.out_semantics = self._check(prefix + "semantics", out_semantics, torch.int32, (p,))
         q.out_kind = self._check(prefix + "kind", out_kind, torch.int32, (p,), optional=True)
+        if self.n_leaves:
+            q.leaves, q.n_leaves = self.leaves.data_ptr(), self.n_leaves
         return q
 
     def point_query(self, points: torch.Tensor, out_distances: torch.Tensor, out_semantics: torch.Tensor, *,

@@ -24,8 +24,10 @@ bbox_max)`` does that at scene load (the reference's ``_load_scene``,
 ``sdfdag_backend.py:1893-1900``); otherwise the first ``cast_rays`` with the
 tensor does it, with a device-to-host copy that waits for the device. Writes
 that bypass the version counter (through ``.data``, or from outside PyTorch)
-need ``invalidate(dag_tensor)``. DAGs the record layout cannot hold (a leaf
-semantic above 0x7fff) and batches above 2^30 rays use the word-layout kernel
+need ``invalidate(dag_tensor)``. Leaves of semantic 0x7fff or above (the
+format's field is 16 bits) go to a leaf table beside the records. DAGs the
+record layout cannot hold (more than 65536 distinct such leaves, or 2^27
+records) and batches above 2^30 rays use the word-layout kernel
 (``navi_cast_rays``), as does ``kernel="raw"``. Results are identical either
 way. Once prepared, a call with ``skip_direction_validation=True`` allocates
 nothing and never waits for the device, as the reference's
@@ -33,6 +35,8 @@ nothing and never waits for the device, as the reference's
 """
 
 from __future__ import annotations
+
+import ctypes
 
 import math
 from typing import Any
@@ -231,15 +235,13 @@ def cast_rays(
     scenes = (_record_layout(dag_tensor, bbox_min, bbox_max)
               if kernel == "auto" and n_rays <= RELAID_MAX_RAYS else None)
     if scenes is not None:
+        # one scene, no scene table or env order (navi_trace_relaid_ex, leaf table included)
+        L = scenes._launch_args(None, None, n_envs, rays, elevation_bins, out_distances.data_ptr(),
+                                out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon)
+        L.origins, L.dirs = origins.data_ptr(), dirs.data_ptr()
         with torch.cuda.device(dev):
             stream = torch.cuda.current_stream(dev).cuda_stream
-            code = _native.lib().navi_trace_relaid(
-                scenes.records.data_ptr(), scenes.n_records, scenes.relaid_table.data_ptr(), 1,
-                scenes.cell_tables.data_ptr(), scenes.table_depth, None, None, n_envs, rays, int(elevation_bins),
-                origins.data_ptr(), dirs.data_ptr(), out_distances.data_ptr(), out_semantics.data_ptr(),
-                int(max_steps), float(max_distance), float(hit_epsilon),
-                out_steps.data_ptr() if out_steps is not None else None, stream,
-            )
+            code = _native.lib().navi_trace_relaid_ex(ctypes.byref(L), stream)
         _native.check(code)
         return
     with torch.cuda.device(dev):

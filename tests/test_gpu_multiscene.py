@@ -362,7 +362,7 @@ def test_relaid_descent_limit_chains(gpu, corpus):
     keeps every slot above depth 32, the second reaches the 32-level limit
     (stale results). Batched alone and together, so both descent loops run."""
     from navi_amd.multiscene import ResidentScenes
-    from tests.test_boundary import _chain_words
+    from tests.test_host_layout import _chain_words
 
     chains = [_chain_words(31), _chain_words(33)]
     rng = np.random.default_rng(5)
@@ -549,7 +549,7 @@ def test_bad_child_index_at_the_descent_limit(gpu, n):
     child: at depth 31 (chain of 31 nodes) the ray reports NaN, at depth 32
     (chain of 32) the 32-level limit comes first and the result is stale."""
     from navi_amd.multiscene import ResidentScenes
-    from tests.test_boundary import _chain_words
+    from tests.test_host_layout import _chain_words
 
     words = _chain_words(n)
     words[2 * n - 1] = words.size + 5  # the last node's child index

@@ -157,7 +157,7 @@ def _same_bits(a, b):
 def test_point_queries(gpu, corpus, depth):
     import torch
 
-    from tests.test_boundary import _chain_words
+    from tests.test_host_layout import _chain_words
 
     chain = _chain_words(33)
     bad = _chain_words(32)

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from tests.test_boundary import _chain_words
+from tests.test_host_layout import _chain_words
 
 
 class _Done:
