@@ -63,14 +63,26 @@ def resident(gpu, corpus):
     return ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus], torch.device("cuda:0"))
 
 
-def test_rooms_512_every_ray(gpu):
-    """64 envs x 256x48 rays on the 512^3 room grid, max 256 steps: every ray."""
+def _small_cases():
+    from navi_amd import workloads as W
+
+    return [(c.name, eps) for c in W.SMALL_CONFIGS for eps in c.hit_epsilons]
+
+
+@pytest.mark.parametrize("name,eps", _small_cases(), ids=lambda v: str(v))
+def test_small_config_every_ray(gpu, name, eps):
+    """The benchmark's smaller workloads with their own seeded ray sets
+    (navi_amd.workloads.single_scene_rays, as bench.py times them): the 64^3 box room
+    (1 env x 64x16 rays, max 64 steps) at hit epsilon 0.01 and 1e-3, the 128^3 cluttered
+    volume (4 envs x 256x48, max 128) and the 512^3 room grid (64 envs x 256x48, max
+    256): every ray of the timed launch shape (staged outputs where the launch stages)
+    and of the launch that returns step counts, and the word counts."""
     import torch
 
     from navi_amd import workloads as W
     from navi_amd.multiscene import ResidentScenes
 
-    cfg = next(c for c in W.SMALL_CONFIGS if c.name == "rooms_512")
+    cfg = next(c for c in W.SMALL_CONFIGS if c.name == name)
     sc = cfg.scene()
     sc.compile(threads=_threads())
     o_np, d_np = W.single_scene_rays(cfg, sc)
@@ -83,22 +95,26 @@ def test_rooms_512_every_ray(gpu):
     out_s = torch.full((E, R), -1, device=dev, dtype=torch.int32)
     out_n = torch.full((E, R), -1, device=dev, dtype=torch.int32)
     out_w = torch.zeros((E, R), device=dev, dtype=torch.int32)
-    _say(f"rooms 512^3: {E * R} rays, relaid kernel")
-    for _ in range(3):  # the first launch measures the scene cost; later ones stage their outputs
-        res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, elevation_bins=cfg.el)
+    what = f"{name} eps {eps:g}"
+    _say(f"{what}: {E * R} rays, relaid kernel")
+    for _ in range(3):  # the timed launch shape: no step counts (outputs staged where the launch stages)
+        res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, elevation_bins=cfg.el)
     torch.cuda.synchronize()
     staged_d, staged_s = out_d.cpu().numpy(), out_s.cpu().numpy()
-    res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, out_steps=out_n, elevation_bins=cfg.el)
+    res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, out_steps=out_n,
+                  elevation_bins=cfg.el)
     torch.cuda.synchronize()
     ref = oracle.trace(sc.words, o_np, d_np, cfg.max_steps, W.MAX_DISTANCE, sc.bbox_min_list, sc.bbox_max,
-                       threads=_threads())
-    _assert_parity(out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), ref, "rooms 512^3")
-    _assert_parity(staged_d, staged_s, out_n.cpu().numpy(), ref, "rooms 512^3, staged outputs")
-    _say("rooms 512^3: word-layout counting kernel")
-    res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, out_words=out_w, kernel="raw")
+                       hit_epsilon=eps, threads=_threads())
+    _assert_parity(out_d.cpu().numpy(), out_s.cpu().numpy(), out_n.cpu().numpy(), ref, what)
+    _assert_parity(staged_d, staged_s, out_n.cpu().numpy(), ref, what + ", timed launch shape")
+    _say(f"{what}: word-layout counting kernel")
+    res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, out_words=out_w,
+                  kernel="raw")
     torch.cuda.synchronize()
-    assert np.array_equal(out_w.cpu().numpy().astype(np.uint64), ref["words"]), "word counts"
-    assert (ref["steps"] > 64).any() and (ref["semantic"] != 0).any()  # long rays and hits both occur
+    assert np.array_equal(out_w.cpu().numpy().astype(np.uint64), ref["words"]), f"{what}: word counts"
+    _assert_parity(out_d.cpu().numpy(), out_s.cpu().numpy(), ref["steps"], ref, what + ", word-layout kernel")
+    assert (ref["semantic"] != 0).any()  # rays hit
 
 
 def test_corpus_batch_every_ray(gpu, corpus, resident):
