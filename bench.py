@@ -16,6 +16,7 @@ observation step (navi_amd/workloads.py defines all of them).
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -28,7 +29,36 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# MI355X: 256 CUs of 4 SIMDs in 8 XCDs; a SIMD issues one wave64 VALU instruction per
+# 4 cycles (16 lanes), at the 2.4 GHz peak engine clock of the published 157.3 TFLOP/s
+# fp32 figure (packed FMA: 4 flops per lane and cycle).
+SIMDS = 256 * 4
+XCDS = 8
+VALU_PEAK = SIMDS * 2.4e9 / 4  # wave64 VALU instructions per second
 CPU_RUNS = 5  # timed oracle runs (after one warm-up); the median is reported
+PROFILE_PATH = ROOT / "profiles" / "tracer_counters.json"
+# the sources of libnavi_trace.so (a counter profile is keyed by their digest)
+TRACER_SOURCES = ("navi_amd/csrc/trace_relaid.hip", "navi_amd/csrc/navi_trace.hip", "navi_amd/csrc/observation.hip",
+                  "navi_amd/csrc/relayout.cpp", "navi_amd/csrc/trace_common.hpp", "navi_amd/csrc/log1p_nonneg.h",
+                  "navi_amd/csrc/Makefile", "include/navi_trace.h")
+# one rocprofv3 run per counter group and workload, each followed by the copy
+# calibration (cd /tmp && export TMPDIR=/tmp first; W = a --profile-workload name)
+PROFILE_COMMANDS = [
+    "rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof/W/kt -o run -- "
+    "python -u bench.py --profile-workload W --copy-calibration-mb 1024",
+    "rocprofv3 --pmc FETCH_SIZE --output-format csv -d gpurun_out/prof/W/fetch -o run -- "
+    "python -u bench.py --profile-workload W --copy-calibration-mb 1024",
+    "rocprofv3 --pmc WRITE_SIZE --output-format csv -d gpurun_out/prof/W/write -o run -- "
+    "python -u bench.py --profile-workload W --copy-calibration-mb 1024",
+    "rocprofv3 --pmc SQ_INSTS_VALU SQ_INSTS_SALU SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR SQ_INSTS_LDS SQ_INSTS_BRANCH "
+    "SQ_WAVES GRBM_GUI_ACTIVE --output-format csv -d gpurun_out/prof/W/sq -o run -- "
+    "python -u bench.py --profile-workload W --copy-calibration-mb 1024",
+    "python bench.py --summarize-profiles gpurun_out/prof profiles/tracer_counters.json",
+]
+PROFILE: dict = {}  # the counter profile's workloads (main loads it)
+PROFILE_CURRENT = False  # whether it was taken on this run's sources
+PROFILE_WORKLOADS = ("headline", "box_room_64@0.01", "box_room_64@0.001", "cluttered_128@0.01", "rooms_512@0.01",
+                     "observation")
 
 
 def _cpu_model() -> str:
@@ -93,17 +123,157 @@ def parity(gd, gs, gn, ref, gw=None) -> dict:
     return out
 
 
-def roofline(alg_bytes: int, ms: float, kernel: str, traffic=None) -> dict:
-    achieved = alg_bytes / (ms / 1e3) / 1e9
-    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
-            "algorithmic_bytes_per_launch": int(alg_bytes)}
+def source_digest() -> str:
+    """First 16 hex digits of the SHA-256 over the tracer library's sources: a counter
+    profile applies to the launches of this run only when it was taken on these."""
+    h = hashlib.sha256()
+    for rel in TRACER_SOURCES:
+        h.update(rel.encode())
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()[:16]
 
 
-def single_scene_config(cfg, dev, threads):
+def load_profile(path: Path) -> tuple[dict, bool]:
+    """The committed counter profile's per-workload entries and whether it was taken on
+    this run's sources ({}, False when there is none)."""
+    if not path.exists():
+        return {}, False
+    prof = json.loads(path.read_text())
+    return prof.get("workloads", {}), prof.get("source_sha16") == source_digest()
+
+
+def roofline(kernel: str, ms: float, alg_bytes: int, counters: dict | None = None, current: bool = False) -> dict:
+    """The dominant kernel against the resource that bounds it, at this run's launch time
+    ``ms``. With a counter profile of the same sources and workload (``counters``):
+    ``bound`` "valu" when VALU issue fills more of the SIMDs' cycles than the measured HBM
+    bytes fill of the HBM peak, else "hbm"; ``achieved`` is VALU wave-instructions (or
+    measured HBM bytes) per launch over ``ms``; the other resource's fraction is given
+    beside it. Without one, ``bound`` is "hbm" and the fractions are null. Either way
+    ``hbm_equivalent`` prices the reference algorithm's DAG-word loads, ray inputs and
+    outputs (``alg_bytes``) at ``ms``: what the reference kernel would move, not a bound
+    of this one (it exceeds the HBM peak where the cell tables, LDS split planes and leaf
+    runs serve those loads on chip)."""
+    s = ms / 1e3
+    eq = alg_bytes / s / 1e9
+    out = {"bound": "hbm", "achieved": None, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": None,
+           "traffic": None, "kernel": kernel,
+           "hbm_equivalent": {"achieved": round(eq, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                              "frac": round(eq / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_launch": int(alg_bytes)},
+           "counters": None}
+    if not counters:
+        return out
+    traffic = counters.get("hbm_bytes_per_launch")
+    valu = counters.get("valu_per_launch")
+    out["counters"] = {"instance": counters.get("instance"), "source_current": current,
+                       "profile_median_ms": counters.get("median_ms"), "valu_per_launch": valu,
+                       "hbm_bytes_per_launch": traffic}
+    if not current:  # taken on other sources: reported, not used
+        return out
+    hbm = None
+    if traffic:
+        hbm = {"achieved": round(traffic / s / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+               "frac": round(traffic / s / 1e9 / HBM_PEAK_GBS, 4)}
+        out["traffic"] = int(traffic)
+    valu_frac = valu / s / VALU_PEAK if valu else None
+    if valu_frac is not None and (hbm is None or valu_frac >= hbm["frac"]):
+        out.update({"bound": "valu", "achieved": round(valu / s / 1e9, 2), "peak": round(VALU_PEAK / 1e9, 1),
+                    "unit": "G VALU wave64-instructions/s", "frac": round(valu_frac, 4), "hbm": hbm})
+    elif hbm is not None:
+        out.update(achieved=hbm["achieved"], frac=hbm["frac"])
+        if valu_frac is not None:
+            out["valu"] = {"achieved": round(valu / s / 1e9, 2), "peak": round(VALU_PEAK / 1e9, 1),
+                           "unit": "G VALU wave64-instructions/s", "frac": round(valu_frac, 4)}
+    return out
+
+
+def summarize_profiles(root: Path, out_path: Path) -> None:
+    """Writes the counter profile from rocprofv3 CSV output under ``root``: one folder per
+    workload (named as bench.py's --profile-workload), each with the sub-folders ``kt``
+    (--kernel-trace), ``fetch`` (--pmc FETCH_SIZE), ``write`` (--pmc WRITE_SIZE) and
+    ``sq`` (--pmc SQ_INSTS_VALU ... GRBM_GUI_ACTIVE). Per workload: the tracer kernel with
+    the most time (and the observation kernel where present), medians over its
+    dispatches; FETCH_SIZE and WRITE_SIZE scaled by what they read for the run's
+    calibration copy (bench.py --copy-calibration-mb)."""
+    import csv
+    import statistics
+
+    def rows(d: Path, suffix: str):
+        files = sorted(d.glob(f"**/*{suffix}"))
+        return list(csv.DictReader(open(files[0]))) if files else []
+
+    def per_dispatch(d: Path):
+        acc: dict = {}
+        for r in rows(d, "counter_collection.csv"):
+            key = (r["Dispatch_Id"], r["Kernel_Name"])
+            acc.setdefault(key, {}).setdefault(r["Counter_Name"], 0.0)
+            acc[key][r["Counter_Name"]] += float(r["Counter_Value"])
+        return acc
+
+    def short(name: str) -> str:
+        return name.split("(")[0].replace("void ", "").replace("navi::", "")
+
+    workloads = {}
+    cal_mib = None
+    for wdir in sorted(p for p in root.iterdir() if p.is_dir()):
+        kt = rows(wdir / "kt", "kernel_trace.csv")
+        if not kt:
+            continue
+        times: dict = {}
+        for r in kt:
+            times.setdefault(r["Kernel_Name"], []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6)
+        tracers = [k for k in times if ("trace_fast_kernel" in k or "trace_relaid_kernel" in k)]
+        kernels = [max(tracers, key=lambda k: sum(times[k]))] if tracers else []
+        kernels += [k for k in times if "observation_kernel" in k]
+        fetch, write, sq = per_dispatch(wdir / "fetch"), per_dispatch(wdir / "write"), per_dispatch(wdir / "sq")
+
+        def scale(acc, counter):
+            cal = [v[counter] for (d, k), v in acc.items() if "copyBuffer" in k and counter in v]
+            return max(cal) if cal else None
+
+        log = (wdir / "cal_mib.txt")
+        mib = int(log.read_text()) if log.exists() else 1024
+        cal_mib = mib
+        f_cal, w_cal = scale(fetch, "FETCH_SIZE"), scale(write, "WRITE_SIZE")
+        f_scale = mib * 1024 / f_cal if f_cal else None
+        w_scale = mib * 1024 / w_cal if w_cal else None
+        for k in kernels:
+            def med(acc, counter):
+                v = [c[counter] for (d, name), c in acc.items() if name == k and counter in c]
+                return statistics.median(v) if v else None
+
+            entry = {"instance": short(k), "dispatches": len(times[k]),
+                     "median_ms": round(statistics.median(times[k]), 5),
+                     "mean_ms": round(statistics.fmean(times[k]), 5)}
+            for c in ("SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR", "SQ_INSTS_LDS",
+                      "SQ_INSTS_BRANCH", "SQ_WAVES", "GRBM_GUI_ACTIVE"):
+                v = med(sq, c)
+                if v is not None:
+                    entry[c] = v
+            fk, wk = med(fetch, "FETCH_SIZE"), med(write, "WRITE_SIZE")
+            if fk is not None and wk is not None and f_scale and w_scale:
+                entry["fetch_kib"], entry["write_kib"] = fk, wk
+                entry["fetch_scale"], entry["write_scale"] = round(f_scale, 5), round(w_scale, 5)
+                entry["hbm_bytes_per_launch"] = int(round((fk * f_scale + wk * w_scale) * 1024))
+            if "SQ_INSTS_VALU" in entry:
+                entry["valu_per_launch"] = entry["SQ_INSTS_VALU"]
+                if "GRBM_GUI_ACTIVE" in entry:
+                    # VALU issue cycles (4 per wave64 instruction) over the SIMDs' cycles
+                    # (GRBM_GUI_ACTIVE sums the dispatch's cycles over the 8 XCDs)
+                    entry["valu_issue_frac"] = round(entry["SQ_INSTS_VALU"] * 4 / SIMDS
+                                                     / (entry["GRBM_GUI_ACTIVE"] / XCDS), 4)
+            name = wdir.name if "observation_kernel" not in k else wdir.name + ":observation_kernel"
+            workloads[name] = entry
+    out = {"source_sha16": source_digest(), "calibration_copy_mib": cal_mib,
+           "valu_peak_per_s": VALU_PEAK, "workloads": workloads,
+           "commands": PROFILE_COMMANDS}
+    out_path.write_text(json.dumps(out, indent=1) + "\n")
+
+
+def single_scene_config(cfg, dev, threads, profile_eps=None):
     """One smaller workload: the record-layout tracer timed per launch, the word-layout
     counting launch for the algorithmic bytes, the oracle timed on the whole ray set, and
-    the parity of the timed kernel's outputs (one entry per hit epsilon)."""
+    the parity of the timed kernel's outputs (one entry per hit epsilon). With
+    ``profile_eps`` only that epsilon's timed launches run (a profiler's workload)."""
     import torch
 
     import oracle
@@ -128,6 +298,10 @@ def single_scene_config(cfg, dev, threads):
             res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps,
                           elevation_bins=cfg.el)
 
+        if profile_eps is not None:
+            if eps == profile_eps:
+                time_launches(launch, 50, 10)
+            continue
         res.cast_rays(es, o, d, out_d, out_s, cfg.max_steps, W.MAX_DISTANCE, hit_epsilon=eps, out_words=out_w,
                       kernel="raw")
         torch.cuda.synchronize()
@@ -151,7 +325,7 @@ def single_scene_config(cfg, dev, threads):
                           "p90": round(float(np.percentile(launches, 90)), 4), "launches": int(launches.size)},
             "rays_per_s": round(E * R / (ms / 1e3), 1),
             "dag_words_per_ray": round(words / (E * R), 3),
-            "roofline": roofline(alg, ms, "trace_fast_kernel"),
+            "roofline": roofline("record-layout tracer", ms, alg, PROFILE.get(f"{cfg.name}@{eps:g}"), PROFILE_CURRENT),
             "cpu_baseline": {"value": round(E * R / t_cpu, 1), "unit": "rays/s", "cores": threads, "kind": "port",
                              "sample": f"the whole ray set ({E * R} rays), median of {CPU_RUNS} runs "
                                        f"after 1 warm-up"},
@@ -186,6 +360,7 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
     ms = ev0.elapsed_time(ev1) / args.obs_steps
     moved = float((walk.pd.view(E, W.POINTS_PER_ENV)[:, 0] >= W.CLEARANCE).float().mean().item())
     observe_ms = float(np.median(time_launches(walk.observe, 20, 3)))
+    trace_ms = float(np.median(time_launches(walk.trace, 20, 3)))
 
     # the final poses: trace and observe once more, then check against the oracle
     walk.trace()
@@ -234,6 +409,7 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
     n_pts = int(pts.shape[0])
     alg = E * R * (24 + 8) + 8 * words + 2 * E * R + n_pts * (12 + 8) + 8 * pw_total
     obs_alg = E * R * (4 + 2) + E * 5 * 4 + E * 4 + n_pts * (12 + 8) + 8 * pw_total
+    trace_alg = E * R * (24 + 8) + 8 * words
     return {
         "workload": f"{E} envs x {W.AZ}x{W.EL} rays from poses, {args.obs_steps} seeded random-walk steps "
                     f"(dpos ~ N(0, 0.05 m), dyaw ~ N(0, 0.1 rad), move kept if its point SDF >= 0.15 m), "
@@ -244,8 +420,14 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
         "entry_points": ["navi_trace_relaid_poses", "navi_observe"],
         "last_step_moves_kept": round(moved, 4),
         "mean_min_distance": round(float(walk.stats[:, 0].mean().item()), 4),
-        "roofline": roofline(alg, ms, "trace_fast_kernel + observation_kernel (whole step)"),
-        "observation_kernel_roofline": roofline(obs_alg, observe_ms, "observation_kernel"),
+        "trace_launch_ms": round(trace_ms, 4),
+        "roofline": roofline("trace_fast_kernel (rays from poses)", trace_ms, trace_alg,
+                             PROFILE.get("observation"), PROFILE_CURRENT),
+        "observation_kernel_roofline": roofline("observation_kernel", observe_ms, obs_alg,
+                                                PROFILE.get("observation:observation_kernel"), PROFILE_CURRENT),
+        "step_hbm_equivalent": {"achieved": round(alg / (ms / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(alg / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                                "algorithmic_bytes_per_step": int(alg)},
         "cpu_baseline": {"value": round(sample.size * R / t_cpu, 1), "unit": "rays/s", "cores": threads,
                          "kind": "port",
                          "sample": f"the last step's rays of {sample.size} envs (the first "
@@ -330,9 +512,19 @@ def main() -> int:
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="first run one device copy of this many MiB (known HBM bytes) so a "
                          "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE run can scale the tracer's counters")
-    ap.add_argument("--traffic-profile", default=str(ROOT / "profiles" / "trace_fast_kernel_traffic.json"),
-                    help="measured HBM bytes per launch (written from rocprofv3 --pmc runs)")
+    ap.add_argument("--profile", default=str(PROFILE_PATH),
+                    help="counter profile of the tracer's launches (bench.py --summarize-profiles writes it)")
+    ap.add_argument("--profile-workload", choices=PROFILE_WORKLOADS,
+                    help="run only this workload's timed launches and print nothing (for rocprofv3)")
+    ap.add_argument("--summarize-profiles", nargs=2, metavar=("PROF_DIR", "OUT_JSON"),
+                    help="write the counter profile from rocprofv3 output (see PROFILE_COMMANDS) and exit")
     args = ap.parse_args()
+
+    global PROFILE, PROFILE_CURRENT
+    if args.summarize_profiles:
+        summarize_profiles(Path(args.summarize_profiles[0]), Path(args.summarize_profiles[1]))
+        return 0
+    PROFILE, PROFILE_CURRENT = load_profile(Path(args.profile))
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -347,6 +539,20 @@ def main() -> int:
     from navi_amd.multiscene import ResidentScenes
 
     n_cpu = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    dev = torch.device("cuda:0")
+    if args.copy_calibration_mb > 0:
+        n_cal = args.copy_calibration_mb * (1 << 20) // 4
+        src = torch.ones(n_cal, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reads and writes exactly copy_calibration_mb MiB each
+        torch.cuda.synchronize()
+        del src, dst
+    if args.profile_workload and "@" in args.profile_workload:
+        name, eps = args.profile_workload.split("@")
+        cfg = next(c for c in W.SMALL_CONFIGS if c.name == name)
+        single_scene_config(cfg, dev, n_cpu, profile_eps=float(eps))
+        torch.cuda.synchronize()
+        return 0
     t0 = time.time()
     seeds = list(range(100, 100 + args.scenes))
     corpus = W.build_corpus(seeds, args.resolution, n_cpu, W.scene_cache_dir(ROOT))
@@ -358,14 +564,6 @@ def main() -> int:
     dirs = S.world_directions(local, yaw)
     origins = np.ascontiguousarray(np.broadcast_to(origins_env[:, None, :], dirs.shape))
 
-    dev = torch.device("cuda:0")
-    if args.copy_calibration_mb > 0:
-        n_cal = args.copy_calibration_mb * (1 << 20) // 4
-        src = torch.ones(n_cal, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)  # reads and writes exactly copy_calibration_mb MiB each
-        torch.cuda.synchronize()
-        del src, dst
     res = ResidentScenes([(c.words, c.bbox_min_list, c.bbox_max) for c in corpus], dev)
     t_es = torch.from_numpy(env_scene).to(dev)
     t_o = torch.from_numpy(origins).to(dev)
@@ -395,10 +593,12 @@ def main() -> int:
         torch.cuda.synchronize()
         return ev0.elapsed_time(ev1) / steps
 
-    # untimed: counts of words the reference algorithm loads (word-layout counting kernel)
-    res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_words=out_w, kernel="raw")
-    torch.cuda.synchronize()
-    total_words = int(out_w.to(torch.int64).sum().item())
+    if args.profile_workload is None:
+        # untimed: counts of words the reference algorithm loads (word-layout counting kernel)
+        res.cast_rays(t_es, t_o, t_d, out_d, out_s, args.max_steps, args.max_distance, out_words=out_w,
+                      kernel="raw")
+        torch.cuda.synchronize()
+        total_words = int(out_w.to(torch.int64).sum().item())
 
     # untimed set-up, whatever --warmup says: the first record-layout launch measures the
     # scenes' costs and a later one adopts the cost order (then cached)
@@ -409,6 +609,16 @@ def main() -> int:
             break
     step()
     torch.cuda.synchronize()
+    if args.profile_workload == "headline":
+        timed("relaid", 12, 3)
+        return 0
+    if args.profile_workload == "observation":
+        walk = W.ObservationWalk(res, env_scene, origins_env, yaw, 16, max_steps=args.max_steps,
+                                 max_distance=args.max_distance)
+        for k in range(16):
+            walk.step(k)
+        torch.cuda.synchronize()
+        return 0
     ms_raw = timed("raw", max(1, args.steps // 4), 1) if not args.no_raw else None
     ms = timed("relaid", args.steps, args.warmup)
     rays_per_s = n_rays / (ms / 1e3)
@@ -458,13 +668,7 @@ def main() -> int:
             _log(f"observation step: {obs['ms_per_step']} ms, parity {obs['parity']}")
         dropin = dropin_timing(corpus, env_scene, t_o, t_d, args)
 
-    traffic = None
-    tp = Path(args.traffic_profile)
-    if tp.exists():
-        prof = json.loads(tp.read_text())
-        if prof.get("workload") == f"{len(corpus)}x{args.resolution}^3/{E}x{R}/{args.max_steps}":
-            traffic = int(prof["hbm_bytes_per_launch"])
-
+    default_workload = (len(corpus), args.resolution, E, R, args.max_steps) == (16, 1024, 1024, 12288, 256)
     line = {
         "metric": "rays/sec on 1 MI355X (256x48 rays/env)",
         "value": round(rays_per_s, 1),
@@ -491,7 +695,8 @@ def main() -> int:
             "mean_steps_per_ray": round(mean_steps, 3), "hit_rate": round(hit_rate, 4),
             "dag_words_per_ray": round(total_words / n_rays, 3),
         },
-        "roofline": roofline(alg_bytes, ms, "trace_fast_kernel", traffic),
+        "roofline": roofline("trace_fast_kernel", ms, alg_bytes, PROFILE.get("headline") if default_workload else None,
+                             PROFILE_CURRENT),
         "cpu_baseline": cpu,
         "parity": par,
         "small_configs": small,
