@@ -324,12 +324,16 @@ def test_relaid_exhaustive_fp16_inline_leaves(gpu):
     assert same.all()
 
 
-def test_relayout_rejects_wide_semantics(gpu):
+def test_relayout_wide_semantics_need_a_leaf_table(gpu):
+    """A semantic beyond the inline slot's 15 bits: navi_relayout refuses it,
+    navi_relayout_leaves puts it in the leaf table (traced in test_gpu_work_queues)."""
     from navi_amd import _native
 
     words = np.array([(1 << 63) | (0x9000 << 16) | 0x3C00], dtype=np.uint64)
-    with pytest.raises(RuntimeError, match="15 bits"):
+    with pytest.raises(RuntimeError, match="leaf table"):
         _native.relayout(words)
+    rec, root, _, leaves = _native.relayout_leaves(words)
+    assert rec.shape[0] == 0 and root == 0xFFFF0000 and leaves.tolist() == [(0x9000 << 16) | 0x3C00]
 
 
 def test_relaid_huge_domains(gpu, corpus):
