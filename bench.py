@@ -210,7 +210,14 @@ def summarize_profiles(root: Path, out_path: Path) -> None:
         return acc
 
     def short(name: str) -> str:
-        return name.split("(")[0].replace("void ", "").replace("navi::", "")
+        # the name without its trailing parameter list (the parenthesis matching the last)
+        depth, cut = 0, len(name)
+        for i in range(len(name) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(name[i], 0)
+            if depth == 0 and name[i] == "(":
+                cut = i
+                break
+        return name[:cut].replace("void ", "").replace("(anonymous namespace)::", "").replace("navi::", "")
 
     workloads = {}
     cal_mib = None
