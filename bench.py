@@ -39,7 +39,8 @@ CPU_RUNS = 5  # timed oracle runs (after one warm-up); the median is reported
 PROFILE_PATH = ROOT / "profiles" / "tracer_counters.json"
 # the sources of libnavi_trace.so (a counter profile is keyed by their digest)
 TRACER_SOURCES = ("navi_amd/csrc/trace_relaid.hip", "navi_amd/csrc/navi_trace.hip", "navi_amd/csrc/observation.hip",
-                  "navi_amd/csrc/relayout.cpp", "navi_amd/csrc/trace_common.hpp", "navi_amd/csrc/log1p_nonneg.h",
+                  "navi_amd/csrc/relayout.cpp", "navi_amd/csrc/errors.cpp", "navi_amd/csrc/trace_common.hpp",
+                  "navi_amd/csrc/log1p_nonneg.h",
                   "navi_amd/csrc/Makefile", "include/navi_trace.h")
 # one rocprofv3 run per counter group and workload, each followed by the copy
 # calibration (cd /tmp && export TMPDIR=/tmp first; W = a --profile-workload name)

@@ -12,4 +12,4 @@ Layers (top to bottom):
 Importing this package does not load the HIP library; the submodules above do.
 """
 
-__version__ = "0.1.0"
+__version__ = "0.3.0"

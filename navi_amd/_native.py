@@ -20,13 +20,45 @@ NAVI_E_LAUNCH = -2
 NAVI_E_LAYOUT = -3
 NAVI_E_NOMEM = -4
 
-if not LIB_PATH.exists():
-    raise ImportError(
-        f"libnavi_trace.so not found at {LIB_PATH}; build it with "
-        "`python -c 'import __graft_entry__ as g; g.build()'` (or `make -C navi_amd/csrc`)."
-    )
 
-_lib = ctypes.CDLL(str(LIB_PATH))
+
+class _HostOnly:
+    """A host-only build of the library's host code (the sanitizer build of
+    ``make -C navi_amd/csrc asan``, named by ``NAVI_HOST_LIB``): the record-layout
+    helpers are there, the device entry points are not (calling one raises)."""
+
+    class _Absent:
+        def __init__(self, name: str) -> None:
+            self.__dict__["name"] = name
+            self.__dict__["argtypes"] = []
+            self.__dict__["restype"] = None
+
+        def __setattr__(self, key, value) -> None:  # argtypes / restype of an absent entry point
+            pass
+
+        def __call__(self, *args):
+            raise RuntimeError(f"{self.name} is not in the host-only library {HOST_LIB_PATH}")
+
+    def __init__(self, path: str) -> None:
+        self._so = ctypes.CDLL(path)
+
+    def __getattr__(self, name: str):
+        try:
+            return getattr(self._so, name)
+        except AttributeError:
+            return _HostOnly._Absent(name)
+
+
+HOST_LIB_PATH = os.environ.get("NAVI_HOST_LIB")
+if HOST_LIB_PATH:
+    _lib = _HostOnly(HOST_LIB_PATH)
+else:
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"libnavi_trace.so not found at {LIB_PATH}; build it with "
+            "`python -c 'import __graft_entry__ as g; g.build()'` (or `make -C navi_amd/csrc`)."
+        )
+    _lib = ctypes.CDLL(str(LIB_PATH))
 
 _vp = ctypes.c_void_p
 _f3 = ctypes.POINTER(ctypes.c_float)

@@ -17,16 +17,8 @@
 
 namespace navi {
 
-thread_local char g_last_error[512] = "";
-
-int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
-int set_error(int code, const char* fmt, ...) {
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
-    va_end(ap);
-    return code;
-}
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));  // errors.cpp
+extern thread_local char g_last_error[512];                                          // errors.cpp
 
 // Bounds-checked word load (kernel.cu:35-41 without the LDS copy, which only
 // caches the same words). Out of range sets `fault`.
@@ -200,10 +192,6 @@ int launch_raw(const uint64_t* pool, uint64_t n_words, Box dom, const navi_scene
 using namespace navi;
 
 extern "C" {
-
-const char* navi_last_error(void) { return g_last_error; }
-
-const char* navi_version(void) { return "0.1.0"; }
 
 int navi_cast_rays(const uint64_t* dag, uint64_t n_words, const float* origins, const float* dirs,
                    float* out_distances, int32_t* out_semantics, int64_t n_rays, int32_t max_steps,

@@ -22,6 +22,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from dataclasses import dataclass, field
 from pathlib import Path
 
@@ -29,7 +30,8 @@ import numpy as np
 
 SPHERE, SOLID_BOX, ROOM = 0, 1, 2
 
-_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libnavi_scene.so"
+# NAVI_SCENE_LIB names another build (the sanitizer build of `make -C navi_amd/csrc asan`)
+_LIB_PATH = Path(os.environ.get("NAVI_SCENE_LIB", Path(__file__).resolve().parent / "_lib" / "libnavi_scene.so"))
 _lib: ctypes.CDLL | None = None
 
 

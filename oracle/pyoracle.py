@@ -89,7 +89,8 @@ def lib() -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    path = _HERE / "liboracle.so"
+    # NAVI_ORACLE_LIB names another build (the sanitizer build of `make -C oracle asan`)
+    path = Path(os.environ.get("NAVI_ORACLE_LIB", _HERE / "liboracle.so"))
     if not path.exists():
         subprocess.run(["make", "-s", "-C", str(_HERE), "liboracle.so"], check=True)
     so = ctypes.CDLL(str(path))
