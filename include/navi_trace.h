@@ -414,6 +414,10 @@ typedef struct navi_observation {
  * ratio (finite and band_min <= c <= band_max; 0 unless band_max > band_min)
  * and forward structure ratio (the same over the first and last
  * max(1, Az / 6) azimuth bins); collision = min c < collision_clearance.
+ * With neither obs nor delta asked for, depth_f16 comes from a log1p of
+ * binary16 accuracy: within one binary16 ulp of the exact depth (as is the
+ * fp16 of the float32 depth otherwise), not always the same bits as the
+ * fp16 of the float32 depth.
  */
 int navi_observe(const navi_observation* observation, const navi_point_queries* queries, void* stream);
 

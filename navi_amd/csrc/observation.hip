@@ -6,17 +6,26 @@
 //
 // Post-pass: one workgroup per env, compiled for the set of outputs asked for.
 // The env's Az * El distances (flat index az * El + el) are read once,
-// coalesced; counts are wave ballots summed on the scalar unit, the minimum a
-// per-lane register; one LDS exchange gives thread 0 the workgroup's totals for
-// the env's statistics. The fp16 depth is written transposed, (env, 1, El, Az),
-// the layout the policy consumes, through an LDS tile with an odd row pitch.
+// coalesced (16-byte loads when Az * El and El are multiples of 4); counts are
+// wave ballots summed on the scalar unit, the minimum a per-lane register; one
+// LDS exchange gives thread 0 the workgroup's totals for the env's statistics.
+// The fp16 depth is written transposed, (env, 1, El, Az), the layout the policy
+// consumes, through an LDS tile with an odd row pitch. The kernel moves
+// 6 bytes per ray (4 read, 2 written) and is bound by HBM: every term of the
+// per-element work is kept to what the scalar and vector units can issue in
+// the time those bytes take, and all workgroups of a 1024-env launch are
+// resident at once (8 waves per SIMD).
 //
 // Point queries: one lane per point, a fresh descent with no caches (the
 // query of kernel.cu:88-200 from the root): the cell table gives the first
-// D levels, record reads the rest.
+// D levels, record reads the rest. Up to 64 points per env ride in the env
+// workgroups (lanes of their first wave, before the env's pass), so that a
+// launch needs no workgroups beyond one per env; more points get workgroups of
+// their own.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdint>
 #include <type_traits>
 
 #include "navi_trace.h"
@@ -65,7 +74,8 @@ struct PostParams {
     float* __restrict__ point_d;
     int32_t* __restrict__ point_s;
     int32_t* __restrict__ point_kind;  // or null
-    int32_t point_blocks;              // workgroups answering point queries; the rest do envs
+    int32_t point_blocks;              // workgroups answering point queries only; the rest do envs
+    int32_t points_per_env;            // > 0: env workgroup e also answers points [e * ppe, (e + 1) * ppe)
     const uint32_t* __restrict__ leaves;  // leaf table (slots 0xffff0000 | i), or null
     uint32_t n_leaves;
 };
@@ -141,6 +151,22 @@ __device__ void point_query(const PostParams& P, int32_t i) {
     if (P.point_kind) P.point_kind[i] = kind;
 }
 
+// log1p(c) for finite c >= 0 (NaN propagates) to the accuracy of the binary16
+// depth, for launches that write no float32 depth: log(1 + c) = log2(u) ln 2 +
+// log(1 + e / u), u = RN(1 + c), e = c - (u - 1) the rounding error of 1 + c
+// (exact). log(1 + e / u) is taken as e (2 - u) for u < 2 (e / u to a relative
+// (u - 1)^2, on a term below 2^-24 / c of the result) and as 0 for u >= 2
+// (below 2^-24 / ln 2 of the result). v_log_f32 is the hardware base-2
+// logarithm, a quarter-rate instruction: this is about a third of the vector
+// instructions of navi_log1p_nonneg. The depth rounded to binary16 is within
+// one binary16 ulp of the exact value for every input (checked on the device
+// for every float in [0, max_distance] against log1p in float64).
+__device__ inline float depth16_log1p(float c) {
+    const float u = 1.0f + c;
+    const float e = c - (u - 1.0f);
+    return fmaf(__builtin_amdgcn_logf(u), 0x1.62e430p-1f, e * fmaxf(2.0f - u, 0.0f));
+}
+
 template <typename T>
 __device__ T block_sum(T v, T* lds) {
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -206,9 +232,69 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
     const int32_t pitch = P.pitch;
     uint32_t n_sat = 0, n_prox = 0, n_band = 0, n_fwd = 0, n_nan = 0;
     float mn = INFINITY;  // of the clamped values; with a NaN input the result is NaN anyway
-    // kBatch coalesced loads in flight per thread before any is used. One
-    // division per batch; then k advances by kThreads = da * El + dr, i.e. r by
-    // dr and a by da, with a carry of one azimuth bin when r wraps.
+    int32_t b0 = 0;
+    // Launches that write only the fp16 depth (and the statistics): 16-byte
+    // loads, lane l holding elements 4l .. 4l + 3 of each 256-element run of
+    // its wave. With El % 4 == 0 the four share an azimuth bin (one tile row,
+    // consecutive columns) and the forward sector (its bounds are multiples of
+    // El), so the row and column are advanced and the sector mask is formed
+    // once per four elements.
+    if constexpr (kF16 == 2 && !kObs && !kDelta) {
+        if ((n & 3) == 0 && (el & 3) == 0 && fwd_lo <= fwd_hi && (reinterpret_cast<uintptr_t>(dist) & 15) == 0) {
+            constexpr int32_t kVec = 3;  // 16-byte loads in flight per thread
+            constexpr int32_t kStep4 = 4 * kThreads * kVec;
+            const int32_t da4 = (4 * kThreads) / el, dr4 = 4 * kThreads - da4 * el;
+            uint64_t nan_any = 0;
+            auto element = [&](float x, uint64_t fwd_mask, int32_t at) {
+                const uint64_t nan = ballot(x != x);
+                const uint64_t valid = ballot(x - x == 0.0f);  // finite
+                const float c = __builtin_amdgcn_fmed3f(x, 0.0f, maxd);
+                mn = fminf(mn, c);
+                nan_any |= nan;
+                n_sat += popc(ballot(c >= sat) & ~nan);
+                n_prox += popc(ballot(c <= prox) & valid);
+                // with band_max <= band_min these counts are not reported
+                const uint64_t in_band = ballot(c >= bmin) & ballot(c <= bmax) & valid;
+                n_band += popc(in_band);
+                n_fwd += popc(in_band & fwd_mask);
+                float lq = depth16_log1p(c);
+                asm volatile("" : "+v"(lq));  // computed for every lane: no branch around it
+                const float q = x != x ? x : fminf(fmaxf(lq * inv, 0.0f), 1.0f);
+                tile[at] = static_cast<_Float16>(q);
+            };
+            for (; b0 + kStep4 <= n; b0 += kStep4) {
+                const float4* d4 = reinterpret_cast<const float4*>(dist + b0);
+                float4 m[kVec];
+#pragma unroll
+                for (int32_t v = 0; v < kVec; ++v) m[v] = d4[tid + v * kThreads];
+                const int32_t k4 = b0 + 4 * tid;
+                int32_t a = k4 / el;
+                int32_t r = k4 - a * el;
+#pragma unroll
+                for (int32_t v = 0; v < kVec; ++v) {
+                    const int32_t kv = k4 + 4 * v * kThreads;
+                    const uint64_t fwd_mask = ballot(kv < fwd_lo || kv >= fwd_hi);
+                    const int32_t at = __umul24(a, pitch) + r;
+                    element(m[v].x, fwd_mask, at);
+                    element(m[v].y, fwd_mask, at + 1);
+                    element(m[v].z, fwd_mask, at + 2);
+                    element(m[v].w, fwd_mask, at + 3);
+                    r += dr4;
+                    a += da4;
+                    if (r >= el) {
+                        r -= el;
+                        ++a;
+                    }
+                    asm volatile("" : "+v"(r), "+v"(a));
+                }
+            }
+            n_nan = nan_any != 0 ? 1u : 0u;  // only whether any is NaN is used
+        }
+    }
+    // The general pass (and what the 16-byte pass leaves): kBatch coalesced
+    // loads in flight per thread before any is used. One division per batch;
+    // then k advances by kThreads = da * El + dr, i.e. r by dr and a by da,
+    // with a carry of one azimuth bin when r wraps.
     constexpr int32_t kBatch = 8;
     const int32_t da = kThreads / el, dr = kThreads - da * el;
     auto run = [&](auto tail, int32_t b0) {
@@ -230,7 +316,7 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
             const float x = m[j];
             // one compare per ballot, combined on the scalar unit
             const uint64_t nan = ballot(x != x) & live;
-            const uint64_t valid = ballot(__builtin_isfinite(x)) & live;
+            const uint64_t valid = ballot(x - x == 0.0f) & live;  // finite
             // torch.clamp(min=0, max=max_distance); NaN lanes are excluded below
             // by their mask, so what the median gives them is never used
             const float c = __builtin_amdgcn_fmed3f(x, 0.0f, maxd);
@@ -243,16 +329,20 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
             // an azimuth bin in both the first and the last Az/6 counts twice, as in torch.cat
             n_fwd += popc(in_band & lanes_below(kw, fwd_lo)) + popc(in_band & ~lanes_below(kw, fwd_hi));
             // sdfdag_backend.py:441-443; c >= 0 here, so the log1p of non-negative
-            // arguments applies (within one ulp of the exact log1p)
-            float lq = navi_log1p_nonneg(c);
-            asm volatile("" : "+v"(lq));  // computed for every lane: no branch around it
-            const float q = x != x ? x : fminf(fmaxf(lq * inv, 0.0f), 1.0f);
+            // arguments applies (within one ulp of the exact log1p, or of the
+            // binary16 depth where only that is written)
+            float q = 0.0f;
+            if constexpr (kObs || kDelta || kF16 != 0) {
+                float lq = (kObs || kDelta) ? navi_log1p_nonneg(c) : depth16_log1p(c);
+                asm volatile("" : "+v"(lq));  // computed for every lane: no branch around it
+                q = x != x ? x : fminf(fmaxf(lq * inv, 0.0f), 1.0f);
+            }
             if (!kTail || k < n) {
                 if constexpr (kObs) {  // sdfdag_backend.py:1516-1524: stack(depth, semantic, valid), (Az, El) order
                     float* ob = O.obs + 3 * base;
                     ob[k] = q;
                     ob[n + k] = static_cast<float>(O.semantics[base + k]);
-                    ob[2 * n + k] = __builtin_isfinite(x) ? 1.0f : 0.0f;
+                    ob[2 * n + k] = x - x == 0.0f ? 1.0f : 0.0f;
                 }
                 if constexpr (kDelta) {  // sdfdag_backend.py:1509-1515
                     const float pv = O.prev_depth[base + k];
@@ -274,7 +364,6 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
         }
     };
     constexpr int32_t kStep = kThreads * kBatch;
-    int32_t b0 = 0;
     for (; b0 + kStep <= n; b0 += kStep) run(std::integral_constant<bool, false>{}, b0);
     if (b0 < n) run(std::integral_constant<bool, true>{}, b0);
     for (int off = 32; off > 0; off >>= 1) mn = fminf(mn, __shfl_xor(mn, off));
@@ -330,17 +419,25 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
 
 // Workgroups [0, point_blocks) answer point queries, one lane each; they come
 // first so that their chains of dependent record reads start with the launch.
-// The rest do the post-pass, one env each.
+// The rest do the post-pass, one env each, the first wave's first
+// points_per_env lanes answering that env's share of the points beforehand.
+// Eight waves per SIMD: four 512-thread workgroups per CU, so that a launch of
+// 1024 envs is resident at once.
 template <bool kObs, bool kDelta, int kF16>
-__global__ __launch_bounds__(kThreads) void observation_kernel(PostParams P) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void observation_kernel(PostParams P) {
     if (static_cast<int32_t>(blockIdx.x) < P.point_blocks) {
         const int32_t i = static_cast<int32_t>(blockIdx.x) * kThreads + threadIdx.x;
         if (i < P.n_points) point_query(P, i);
         return;
     }
+    const int32_t e = static_cast<int32_t>(blockIdx.x) - P.point_blocks;
+    if (static_cast<int32_t>(threadIdx.x) < P.points_per_env) {
+        const int64_t i = static_cast<int64_t>(e) * P.points_per_env + threadIdx.x;
+        if (i < P.n_points) point_query(P, static_cast<int32_t>(i));
+    }
     extern __shared__ _Float16 tile[];  // the env's fp16 tile when staged
     __shared__ uint32_t red[kRed * (kThreads / 64)];
-    observe_env<kObs, kDelta, kF16>(P, static_cast<int32_t>(blockIdx.x) - P.point_blocks, tile, red);
+    observe_env<kObs, kDelta, kF16>(P, e, tile, red);
 }
 
 template <bool kObs, bool kDelta, int kF16>
@@ -359,7 +456,13 @@ int launch_f16(const PostParams& P, hipStream_t stream, unsigned blocks, size_t 
 }
 
 int launch(PostParams& P, hipStream_t stream) {
-    const int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
+    int64_t point_blocks = (static_cast<int64_t>(P.n_points) + kThreads - 1) / kThreads;
+    P.points_per_env = 0;
+    if (P.n_envs > 0 && P.n_points > 0 && static_cast<int64_t>(P.n_points) <= 64LL * P.n_envs) {
+        // every env workgroup takes up to 64 points: no extra workgroups
+        P.points_per_env = static_cast<int32_t>((static_cast<int64_t>(P.n_points) + P.n_envs - 1) / P.n_envs);
+        point_blocks = 0;
+    }
     const int64_t blocks = static_cast<int64_t>(P.n_envs) + point_blocks;
     if (blocks == 0) return NAVI_OK;
     P.point_blocks = static_cast<int32_t>(point_blocks);

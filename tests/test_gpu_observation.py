@@ -5,7 +5,11 @@ queries (navi_point_query) and the fused post-pass (navi_observe).
 Bars: traced rays as in test_gpu_multiscene (bit-exact); point queries
 bit-exact (distance bits, semantic, kind); post-pass min distance and
 collision exact, ratios within 1e-6, fp16 depth within one binary16 ulp,
-float32 depth within DEPTH_RTOL of the oracle's.
+float32 depth within DEPTH_RTOL of the oracle's. A launch that writes no
+float32 depth computes the fp16 depth with a binary16-accuracy log1p
+(depth16_log1p in navi_amd/csrc/observation.hip): within one binary16 ulp of
+the exact value for every float input in [0, max_distance], checked here
+exhaustively for max_distance 30.
 """
 
 from __future__ import annotations
@@ -241,16 +245,18 @@ def test_observe_matches_oracle(gpu, corpus, az, el, band):
                 out_stats=st, out_collision=co, semantics=ts, out_obs=obs, prev_depth=tprev, out_delta=delta)
     torch.cuda.synchronize()
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
-    # the same with only the fp16 depth and the statistics (the observation step's outputs),
-    # a kernel compiled without the float32 outputs
+    # the same with only the fp16 depth and the statistics (the observation step's outputs):
+    # a kernel compiled without the float32 outputs, its depth from the binary16-accuracy
+    # log1p; statistics and collision identical, the fp16 depth to the same bar
     d16b = torch.empty_like(d16)
     stb = torch.empty_like(st)
     cob = torch.empty_like(co)
     res.observe(td, az, el, 30.0, structure_band_min=band[0], structure_band_max=band[1], out_depth_f16=d16b,
                 out_stats=stb, out_collision=cob)
     torch.cuda.synchronize()
-    assert torch.equal(d16b.view(torch.int16), d16.view(torch.int16))
     assert torch.equal(stb.view(torch.int32), st.view(torch.int32)) and torch.equal(cob, co)
+    _observe_oracle_check((d16b.cpu().numpy(), stb.cpu().numpy(), cob.cpu().numpy()), want)
+    assert int((d16b.view(torch.int16).int() - d16.view(torch.int16).int()).abs().max()) <= 1
     # float32 outputs: depth within DEPTH_RTOL, semantic / valid exact
     go = obs.cpu().numpy()
     np.testing.assert_array_equal(go[:, 1:], want["obs"][:, 1:])
@@ -303,6 +309,78 @@ def test_observe_depth_against_exact_log1p(gpu, corpus):
     assert (np.abs(h - h_exact.astype(np.float64)) <= ulp).all()
 
 
+def _rn16(torch, exact):
+    """float64 -> the nearest binary16 (one rounding): the float32 cast's result or a
+    neighbour of it, whichever is nearest to the exact value."""
+    h = exact.float().half().view(torch.int16).int()
+    best, pick = None, None
+    for dlt in (-1, 0, 1):
+        cand = (h + dlt).clamp(0, 0x7BFF).short().view(torch.float16)
+        err = (cand.double() - exact).abs()
+        if best is None:
+            best, pick = err, cand
+        else:
+            better = err < best
+            best, pick = torch.where(better, err, best), torch.where(better, cand, pick)
+    return pick
+
+
+def test_fp16_depth_every_float(gpu, corpus):
+    """The fp16-only launch (no float32 depth asked for: the observation step's) over
+    every binary32 c in [0, 30], 1.1e9 inputs as 256 x 48 envs: the fp16 depth within one
+    binary16 ulp of RN16(log1p(c) / log1p(30)), the quotient in float64 (device log1p).
+    Then the same envs through the general pass (the distances at an address that is not
+    16-byte aligned): the same fp16 depth and statistics, bit for bit."""
+    import torch
+
+    az, el = 256, 48
+    n = az * el
+    res = _resident(corpus)
+    dev = res.device
+    top = int(np.float32(30.0).view(np.uint32))
+    chunk = (1 << 28) // n * n
+    not_rn, worst = 0, 0
+    for lo in range(0, top + 1, chunk):
+        e = -(-min(chunk, top + 1 - lo) // n)
+        bits = torch.arange(lo, lo + e * n, device=dev, dtype=torch.int64).clamp_(max=top).to(torch.int32)
+        c = bits.view(torch.float32).view(e, n)
+        d16 = torch.empty((e, 1, el, az), dtype=torch.float16, device=dev)
+        res.observe(c, az, el, 30.0, out_depth_f16=d16)
+        want = _rn16(torch, torch.log1p(c.double()) / math.log1p(30.0))
+        got = d16.view(e, el, az).transpose(1, 2).reshape(e, n)
+        diff = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs()
+        not_rn += int((diff != 0).sum())
+        worst = max(worst, int(diff.max()))
+        del bits, want, diff
+    assert worst <= 1, f"fp16 depth {worst} binary16 ulps from the exact value"
+    assert not_rn < 100_000  # about 1.3e-5 of the inputs differ from RN16(exact), by one ulp
+    # general pass against the 16-byte pass, with NaN, infinities and statistics
+    rng = np.random.default_rng(11)
+    e = 64
+    d = rng.uniform(-1.0, 40.0, (e, n)).astype(np.float32)
+    d[0, :6] = [np.inf, -np.inf, np.nan, 0.0, 30.0, 29.999]
+    d[5, 100] = np.nan
+    d[7] = rng.uniform(0.0, 0.3, n)
+    aligned = torch.from_numpy(d).to(dev)
+    store = torch.empty(e * n + 1, device=dev)
+    shifted = store[1:].view(e, n)
+    shifted.copy_(aligned)
+    assert aligned.data_ptr() % 16 == 0 and shifted.data_ptr() % 16 == 4
+    outs = []
+    for src in (aligned, shifted):
+        d16 = torch.empty((e, 1, el, az), dtype=torch.float16, device=dev)
+        st = torch.empty((e, 5), device=dev)
+        co = torch.empty((e,), dtype=torch.int32, device=dev)
+        res.observe(src, az, el, 30.0, out_depth_f16=d16, out_stats=st, out_collision=co)
+        outs.append((d16, st, co))
+    torch.cuda.synchronize()
+    (a16, ast, aco), (b16, bst, bco) = outs
+    assert torch.equal(a16.view(torch.int16), b16.view(torch.int16))
+    assert torch.equal(ast.view(torch.int32), bst.view(torch.int32)) and torch.equal(aco, bco)
+    want = oracle.observe(d, az, el, 30.0, 1.5, 30.0, 2.0, 0.15)
+    _observe_oracle_check((a16.cpu().numpy(), ast.cpu().numpy(), aco.cpu().numpy()), want)
+
+
 def test_observation_step_end_to_end(gpu, corpus):
     """Poses -> traced rays -> fused post-pass with point queries, against the oracle
     pipeline on the same inputs."""
@@ -340,6 +418,29 @@ def test_observation_step_end_to_end(gpu, corpus):
     _observe_oracle_check((d16.cpu().numpy(), st.cpu().numpy(), co.cpu().numpy()), want)
     assert np.array_equal(pk.cpu().numpy(), pwant[2]) and np.array_equal(ps.cpu().numpy(), pwant[1])
     assert _same_bits(pd.cpu().numpy(), pwant[0])
+    # 64 points per env (the most that ride in the env workgroups), 65 (workgroups of
+    # their own) and 3 for 12 envs (some env workgroups take none): the same answers
+    for per_env in (64, 65):
+        m = per_env * e
+        mp = (np.repeat(pos, per_env, axis=0) + rng.uniform(-0.3, 0.3, (m, 3))).astype(np.float32)
+        msc = np.repeat(env_scene, per_env).astype(np.int32)
+        mw = _point_oracle([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus], msc, mp)
+        md, ms, mk = (torch.empty((m,), device=dev), torch.empty((m,), device=dev, dtype=torch.int32),
+                      torch.empty((m,), device=dev, dtype=torch.int32))
+        res.observe(out_d, az, el, 30.0, out_depth_f16=d16, points=torch.from_numpy(mp).to(dev),
+                    point_scene=torch.from_numpy(msc).to(dev), point_distances=md, point_semantics=ms,
+                    point_kind=mk)
+        torch.cuda.synchronize()
+        assert np.array_equal(mk.cpu().numpy(), mw[2]) and np.array_equal(ms.cpu().numpy(), mw[1])
+        assert _same_bits(md.cpu().numpy(), mw[0])
+    few = (pos[:3] + 0.01).astype(np.float32)
+    fsc = env_scene[:3].astype(np.int32)
+    fw = _point_oracle([c.words for c in corpus], [c.bbox_min_list + c.bbox_max for c in corpus], fsc, few)
+    fd, fs = torch.empty((3,), device=dev), torch.empty((3,), device=dev, dtype=torch.int32)
+    res.observe(out_d, az, el, 30.0, out_depth_f16=d16, points=torch.from_numpy(few).to(dev),
+                point_scene=torch.from_numpy(fsc).to(dev), point_distances=fd, point_semantics=fs)
+    torch.cuda.synchronize()
+    assert np.array_equal(fs.cpu().numpy(), fw[1]) and _same_bits(fd.cpu().numpy(), fw[0])
 
 
 def test_bench_sdfdag_harness(gpu, tmp_path, capsys):
