@@ -22,7 +22,9 @@ and uploaded, keyed by the tensor object, its version counter (in-place tensor
 ops invalidate it), its address and the bbox. ``prepare(dag_tensor, bbox_min,
 bbox_max)`` does that at scene load (the reference's ``_load_scene``,
 ``sdfdag_backend.py:1893-1900``); otherwise the first ``cast_rays`` with the
-tensor does it, with a device-to-host copy that waits for the device. Writes
+tensor does it, with a device-to-host copy that waits for the device, and warns
+(``LayoutConversionWarning``, once per call site under Python's default warning
+filter; ``conversion_counts()`` counts every conversion). Writes
 that bypass the version counter (through ``.data``, or from outside PyTorch)
 need ``invalidate(dag_tensor)``. Leaves of semantic 0x7fff or above (the
 format's field is 16 bits) go to a leaf table beside the records. DAGs the
@@ -45,6 +47,7 @@ import numpy as np
 import torch
 
 import threading
+import warnings
 import weakref
 
 from . import _native
@@ -54,7 +57,13 @@ HIT_EPSILON = 0.01  # kernel.cuh:7
 _INT32_MAX = 0x7FFFFFFF
 RELAID_MAX_RAYS = 1 << 30  # rays per navi_trace_relaid launch; larger batches take navi_cast_rays
 
-__all__ = ["cast_rays", "prepare", "invalidate", "HIT_EPSILON"]
+__all__ = ["cast_rays", "prepare", "invalidate", "conversion_counts", "LayoutConversionWarning", "HIT_EPSILON"]
+
+
+class LayoutConversionWarning(RuntimeWarning):
+    """``cast_rays`` converted a DAG tensor to the record layout inside the call: a
+    device-to-host copy that waits for the device, a host relayout and an upload.
+    ``prepare()`` at scene load moves that work out of the step."""
 
 
 def _check(cond: bool, msg: str) -> None:
@@ -161,9 +170,10 @@ class _RecordLayout:
 
 _layout_lock = threading.Lock()
 _layouts: dict[int, _RecordLayout] = {}
+_conversions = {"prepare": 0, "cast_rays": 0}
 
 
-def _record_layout(dag_tensor: torch.Tensor, bbox_min, bbox_max):
+def _record_layout(dag_tensor: torch.Tensor, bbox_min, bbox_max, caller: str):
     bounds = (tuple(_f32(v) for v in bbox_min), tuple(_f32(v) for v in bbox_max))
     with _layout_lock:
         entry = _layouts.get(id(dag_tensor))
@@ -172,7 +182,20 @@ def _record_layout(dag_tensor: torch.Tensor, bbox_min, bbox_max):
                 del _layouts[key]
             entry = _RecordLayout(dag_tensor, bounds)
             _layouts[id(dag_tensor)] = entry
+            _conversions[caller] += 1
+            if caller == "cast_rays":
+                warnings.warn(
+                    f"cast_rays converted a {dag_tensor.numel()}-word DAG tensor to the record layout inside the "
+                    "call (a device-to-host copy that waits for the device); call torch_sdf.prepare(dag_tensor, "
+                    "bbox_min, bbox_max) when the scene is loaded", LayoutConversionWarning, stacklevel=4)
         return entry.scenes
+
+
+def conversion_counts() -> dict[str, int]:
+    """How many record-layout conversions ``prepare`` and ``cast_rays`` have done in this
+    process (a conversion inside ``cast_rays`` waits for the device)."""
+    with _layout_lock:
+        return dict(_conversions)
 
 
 def prepare(dag_tensor: torch.Tensor, bbox_min, bbox_max) -> bool:
@@ -185,7 +208,7 @@ def prepare(dag_tensor: torch.Tensor, bbox_min, bbox_max) -> bool:
     _check(dag_tensor.is_contiguous(), "dag_tensor must be contiguous")
     _validate_bounds(bbox_min, bbox_max)
     _native.device_init(dag_tensor.device)
-    return _record_layout(dag_tensor, bbox_min, bbox_max) is not None
+    return _record_layout(dag_tensor, bbox_min, bbox_max, "prepare") is not None
 
 
 def invalidate(dag_tensor: torch.Tensor | None = None) -> None:
@@ -232,7 +255,7 @@ def cast_rays(
     n_envs, rays = int(origins.size(0)), int(origins.size(1))
     n_rays = n_envs * rays
     dev = dag_tensor.device
-    scenes = (_record_layout(dag_tensor, bbox_min, bbox_max)
+    scenes = (_record_layout(dag_tensor, bbox_min, bbox_max, "cast_rays")
               if kernel == "auto" and n_rays <= RELAID_MAX_RAYS else None)
     if scenes is not None:
         # one scene, no scene table or env order (navi_trace_relaid_ex, leaf table included)

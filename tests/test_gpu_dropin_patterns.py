@@ -218,3 +218,45 @@ def test_side_stream_step_sequence(torch_sdf, scene, resident):
         for s, sc in enumerate(scenes):
             envs = np.flatnonzero(env_scene == s)
             _check(sc, o_np[envs], d_np[envs], od[envs], os_[envs], 128, f"step {k} scene {s}")
+
+
+def test_conversion_inside_a_call_warns(torch_sdf, scene):
+    """A DAG tensor that was not prepared is converted inside ``cast_rays`` (a
+    device-to-host copy that waits): the call warns and counts it; later calls with the
+    same tensor, and calls with a prepared tensor, convert nothing and do not warn."""
+    import warnings
+
+    import torch
+
+    from navi_amd import scenes as S
+    from navi_amd import torch_sdf_backend as B
+
+    dev = torch.device("cuda:0")
+    sc = scene
+    dirs_np = np.repeat(S.canonical_directions(16, 4)[None], 3, axis=0)
+    lo, hi = np.array(sc.bbox_min_list, np.float32), np.array(sc.bbox_max, np.float32)
+    pts = (lo + (hi - lo) * np.array([[0.3, 0.4, 0.5], [0.5, 0.5, 0.5], [0.7, 0.6, 0.4]], np.float32))
+    origins_np = np.ascontiguousarray(np.repeat(pts.astype(np.float32)[:, None, :], dirs_np.shape[1], axis=1))
+    origins = torch.from_numpy(origins_np).to(dev)
+    dirs = torch.from_numpy(dirs_np).to(dev)
+    out_d = torch.empty(dirs.shape[:2], device=dev)
+    out_s = torch.empty(dirs.shape[:2], device=dev, dtype=torch.int32)
+
+    def cast(dag):
+        torch_sdf.cast_rays(dag, origins, dirs, out_d, out_s, 96, 30.0, sc.bbox_min_list, list(sc.bbox_max),
+                            sc.resolution)
+
+    before = B.conversion_counts()
+    unprepared = torch.from_numpy(sc.words.view(np.int64).copy()).to(dev)
+    with pytest.warns(B.LayoutConversionWarning, match="prepare"):
+        cast(unprepared)
+    _check(sc, origins_np, dirs_np, out_d, out_s, 96, "converted in the call")
+    prepared = torch.from_numpy(sc.words.view(np.int64).copy()).to(dev)
+    assert torch_sdf.prepare(prepared, sc.bbox_min_list, list(sc.bbox_max))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", B.LayoutConversionWarning)
+        cast(unprepared)
+        cast(prepared)
+    _check(sc, origins_np, dirs_np, out_d, out_s, 96, "prepared")
+    after = B.conversion_counts()
+    assert after["cast_rays"] - before["cast_rays"] == 1 and after["prepare"] - before["prepare"] == 1
