@@ -95,6 +95,38 @@ def time_launches(fn, launches: int, warmup: int):
     return np.array([evs[k].elapsed_time(evs[k + 1]) for k in range(launches)])
 
 
+def time_graph(fn, calls: int, replays: int):
+    """``calls`` calls of ``fn`` captured into one HIP graph (launched back to back, no host
+    in between), the graph replayed ``replays`` times between HIP events on the current
+    stream: per-call times in ms, one per replay. For kernels shorter than a host launch,
+    where events around single launches also time the dispatch."""
+    import torch
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()  # warm-up on the capture's stream
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    out = []
+    for _ in range(replays):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b) / calls)
+    del graph
+    return np.array(out)
+
+
 def time_cpu(fn):
     """One warm-up, then the median of CPU_RUNS timed calls (s); returns (median, last result)."""
     out = fn()
@@ -368,6 +400,9 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
     ms = ev0.elapsed_time(ev1) / args.obs_steps
     moved = float((walk.pd.view(E, W.POINTS_PER_ENV)[:, 0] >= W.CLEARANCE).float().mean().item())
     observe_ms = float(np.median(time_launches(walk.observe, 20, 3)))
+    # the post-pass kernel alone: 32 launches back to back in a graph (events around one
+    # launch of ~20 us also time its dispatch)
+    observe_kernel_ms = float(np.median(time_graph(walk.observe, 32, 5)))
     trace_ms = float(np.median(time_launches(walk.trace, 20, 3)))
 
     # the final poses: trace and observe once more, then check against the oracle
@@ -425,13 +460,14 @@ def observation_walk(res, corpus, env_scene, origins_env, yaw, args, threads, cp
         "rays_per_s": round(E * R / (ms / 1e3), 1),
         "ms_per_step": round(ms, 4),
         "observe_launch_ms": round(observe_ms, 4),
+        "observe_kernel_ms": round(observe_kernel_ms, 4),
         "entry_points": ["navi_trace_relaid_poses", "navi_observe"],
         "last_step_moves_kept": round(moved, 4),
         "mean_min_distance": round(float(walk.stats[:, 0].mean().item()), 4),
         "trace_launch_ms": round(trace_ms, 4),
         "roofline": roofline("trace_fast_kernel (rays from poses)", trace_ms, trace_alg,
                              PROFILE.get("observation"), PROFILE_CURRENT),
-        "observation_kernel_roofline": roofline("observation_kernel", observe_ms, obs_alg,
+        "observation_kernel_roofline": roofline("observation_kernel", observe_kernel_ms, obs_alg,
                                                 PROFILE.get("observation:observation_kernel"), PROFILE_CURRENT),
         "step_hbm_equivalent": {"achieved": round(alg / (ms / 1e3) / 1e9, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                 "frac": round(alg / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -379,20 +379,41 @@ __device__ void observe_env(const PostParams& P, int32_t e, _Float16* tile, uint
     }
     __syncthreads();
     if constexpr (kF16 == 2) {
-        // Az is even: halves t and t + 1 share r, at tile[a * pitch + r] and pitch further
-        uint32_t* out = reinterpret_cast<uint32_t*>(static_cast<_Float16*>(O.depth_f16) + base);
+        _Float16* const out16 = static_cast<_Float16*>(O.depth_f16) + base;
         const uint16_t* src = reinterpret_cast<const uint16_t*>(tile);
-        int32_t r = (2 * tid) / az;
-        int32_t a = 2 * tid - r * az;
-        const int32_t dr2 = (2 * kThreads) / az, da2 = 2 * kThreads - dr2 * az;
-        for (int32_t i = tid; i < n / 2; i += kThreads) {
-            const int32_t at = __umul24(a, pitch) + r;
-            out[i] = static_cast<uint32_t>(src[at]) | (static_cast<uint32_t>(src[at + pitch]) << 16);
-            r += dr2;
-            a += da2;
-            if (a >= az) {
-                a -= az;
-                ++r;
+        if ((az & 3) == 0 && (reinterpret_cast<uintptr_t>(out16) & 7) == 0) {
+            // Az % 4 == 0: halves t .. t + 3 (t = 4i) share r, at tile[a * pitch + r] and
+            // pitch, 2 pitch, 3 pitch further; one 8-byte store per lane
+            uint2* out = reinterpret_cast<uint2*>(out16);
+            int32_t r = (4 * tid) / az;
+            int32_t a = 4 * tid - r * az;
+            const int32_t dr4 = (4 * kThreads) / az, da4 = 4 * kThreads - dr4 * az;
+            for (int32_t i = tid; i < n / 4; i += kThreads) {
+                const int32_t at = __umul24(a, pitch) + r;
+                const uint32_t h0 = src[at], h1 = src[at + pitch], h2 = src[at + 2 * pitch], h3 = src[at + 3 * pitch];
+                out[i] = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+                r += dr4;
+                a += da4;
+                if (a >= az) {
+                    a -= az;
+                    ++r;
+                }
+            }
+        } else {
+            // Az is even: halves t and t + 1 share r, at tile[a * pitch + r] and pitch further
+            uint32_t* out = reinterpret_cast<uint32_t*>(out16);
+            int32_t r = (2 * tid) / az;
+            int32_t a = 2 * tid - r * az;
+            const int32_t dr2 = (2 * kThreads) / az, da2 = 2 * kThreads - dr2 * az;
+            for (int32_t i = tid; i < n / 2; i += kThreads) {
+                const int32_t at = __umul24(a, pitch) + r;
+                out[i] = static_cast<uint32_t>(src[at]) | (static_cast<uint32_t>(src[at + pitch]) << 16);
+                r += dr2;
+                a += da2;
+                if (a >= az) {
+                    a -= az;
+                    ++r;
+                }
             }
         }
     }

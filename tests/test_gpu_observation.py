@@ -330,7 +330,8 @@ def test_fp16_depth_every_float(gpu, corpus):
     every binary32 c in [0, 30], 1.1e9 inputs as 256 x 48 envs: the fp16 depth within one
     binary16 ulp of RN16(log1p(c) / log1p(30)), the quotient in float64 (device log1p).
     Then the same envs through the general pass (the distances at an address that is not
-    16-byte aligned): the same fp16 depth and statistics, bit for bit."""
+    16-byte aligned) and through the two-half copy-out (an fp16 output that is not 8-byte
+    aligned): the same fp16 depth and statistics, bit for bit."""
     import torch
 
     az, el = 256, 48
@@ -377,6 +378,14 @@ def test_fp16_depth_every_float(gpu, corpus):
     (a16, ast, aco), (b16, bst, bco) = outs
     assert torch.equal(a16.view(torch.int16), b16.view(torch.int16))
     assert torch.equal(ast.view(torch.int32), bst.view(torch.int32)) and torch.equal(aco, bco)
+    # an fp16 output 4 bytes off an 8-byte boundary: copied out two halves per lane
+    # instead of four, same bits
+    store16 = torch.empty(e * n + 2, dtype=torch.float16, device=dev)
+    c16 = store16[2:].view(e, 1, el, az)
+    assert c16.data_ptr() % 8 == 4
+    res.observe(aligned, az, el, 30.0, out_depth_f16=c16)
+    torch.cuda.synchronize()
+    assert torch.equal(c16.view(torch.int16), a16.view(torch.int16))
     want = oracle.observe(d, az, el, 30.0, 1.5, 30.0, 2.0, 0.15)
     _observe_oracle_check((a16.cpu().numpy(), ast.cpu().numpy(), aco.cpu().numpy()), want)
 
