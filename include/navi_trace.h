@@ -302,6 +302,14 @@ int navi_trace_relaid_poses(const uint32_t* records, uint64_t n_records, const n
                             int32_t max_steps, float max_distance, float hit_epsilon, int32_t* out_steps,
                             void* stream);
 
+/* Element type of navi_relaid_launch.out_distances. The march accumulates in
+ * float32 either way; a finished ray's distance is rounded to nearest even
+ * (NaN as 0x7fc0 in bfloat16, a quiet NaN in float16). The reference's roadmap
+ * item for this output: docs/FUTURE_HARDWARE_ROADMAP.md:140-222. */
+#define NAVI_DIST_F32 0   /* float */
+#define NAVI_DIST_BF16 1  /* bfloat16 (uint16 storage) */
+#define NAVI_DIST_F16 2   /* IEEE binary16 */
+
 /* Arguments of navi_trace_relaid_ex (device pointers unless noted). */
 typedef struct navi_relaid_launch {
     const uint32_t* records;           /* record pool, as navi_trace_relaid */
@@ -322,18 +330,20 @@ typedef struct navi_relaid_launch {
     const float* local_dirs;           /* rays from poses, as navi_trace_relaid_poses */
     const float* env_pos;
     const float* env_rot;
-    float* out_distances;
+    void* out_distances;               /* [n_rays] of distance_dtype */
     int32_t* out_semantics;
     int32_t* out_steps;                /* or NULL */
     int32_t max_steps;
     float max_distance;
     float hit_epsilon;
+    int32_t distance_dtype;            /* NAVI_DIST_* (0: float) */
 } navi_relaid_launch;
 
 /*
  * navi_trace_relaid / navi_trace_relaid_poses with every argument in one
  * struct (no reference counterpart), adding the leaf table for semantics of
- * 0x7fff and above (the format's 16-bit field, docs/GMDAG.md:215,223).
+ * 0x7fff and above (the format's 16-bit field, docs/GMDAG.md:215,223) and
+ * distances as bfloat16 or float16 (distance_dtype).
  */
 int navi_trace_relaid_ex(const navi_relaid_launch* launch, void* stream);
 

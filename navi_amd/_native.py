@@ -132,7 +132,7 @@ class RelaidLaunch(ctypes.Structure):
                 ("elevation_bins", ctypes.c_int32), ("origins", _vp), ("dirs", _vp), ("local_dirs", _vp),
                 ("env_pos", _vp), ("env_rot", _vp), ("out_distances", _vp), ("out_semantics", _vp),
                 ("out_steps", _vp), ("max_steps", ctypes.c_int32), ("max_distance", ctypes.c_float),
-                ("hit_epsilon", ctypes.c_float)]
+                ("hit_epsilon", ctypes.c_float), ("distance_dtype", ctypes.c_int32)]
 
 
 class LaunchInfo(ctypes.Structure):
@@ -175,6 +175,7 @@ RELAID_SCENE_DTYPE = [("rec_offset", "<u8"), ("n_records", "<u4"), ("root_slot",
                       ("bbox_min", "<f4", (3,)), ("bbox_max", "<f4", (3,)), ("max_depth", "<u4"),
                       ("flags", "<u4")]
 SCENE_NONNEG_LEAVES = 1  # navi_relaid_scene.flags bit (include/navi_trace.h)
+DIST_F32, DIST_BF16, DIST_F16 = 0, 1, 2  # navi_relaid_launch.distance_dtype
 
 
 def scene_flags(records, root_slot, leaves=None) -> int:

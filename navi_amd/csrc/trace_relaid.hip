@@ -122,7 +122,7 @@ struct RelaidParams {
     const float* __restrict__ local_dirs;  // [rays_per_env][3]
     const float* __restrict__ env_pos;     // [n_envs][3]
     const float* __restrict__ env_rot;     // [n_envs][2]
-    float* __restrict__ out_d;
+    float* __restrict__ out_d;  // of dist_dtype elements
     int32_t* __restrict__ out_s;
     int32_t* __restrict__ out_steps;
     int32_t max_steps;
@@ -133,6 +133,7 @@ struct RelaidParams {
     uint32_t n_units;              // work units of unit_rays rays
     uint32_t unit_rays;            // 128 (2 tiles), or 64 for batches too small to fill the chip
     uint32_t small_tables;         // the cell tables span fewer than 2^32 bytes
+    uint32_t dist_dtype;           // NAVI_DIST_*: out_d holds float, bfloat16 or float16
     uint32_t stage;                // finished rays staged per tile in LDS (fast march)
     uint32_t after_fast;           // launched after trace_fast_kernel: return if that one ran
     // leaf table of the leaves of semantic 0x7fff or above (slot 0xffff0000 | i
@@ -178,6 +179,24 @@ __device__ __forceinline__ float markstein(float a, float b, float r) {
     const float q0 = a * r;
     const float e = __builtin_fmaf(-q0, b, a);
     return __builtin_fmaf(e, r, q0);
+}
+
+// A finished ray's distance into out_d[i] as the launch's element type:
+// float, or rounded to nearest even to bfloat16 (NaN as 0x7fc0) or float16.
+// Non-temporal: lines of these scattered stores do not stay in L2.
+__device__ __forceinline__ void store_distance(const RelaidParams& P, uint32_t i, float t) {
+    if (P.dist_dtype == NAVI_DIST_F32) {
+        __builtin_nontemporal_store(t, &P.out_d[i]);
+        return;
+    }
+    uint16_t h;
+    if (P.dist_dtype == NAVI_DIST_BF16) {
+        const uint32_t u = __float_as_uint(t);
+        h = (t != t) ? static_cast<uint16_t>(0x7fc0u) : static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+    } else {
+        h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(t));
+    }
+    __builtin_nontemporal_store(h, reinterpret_cast<uint16_t*>(P.out_d) + i);
 }
 
 // LDS addresses as 32-bit byte offsets (the local address space) and back
@@ -472,7 +491,7 @@ __device__ __forceinline__ int start_ray(const RelaidParams& P, uint32_t q, RayS
     R.rz = (R.dz > kDirEps || R.dz < -kDirEps) ? 1.0f / R.dz : __builtin_nanf("");
     if (sc < 0 || sc >= P.n_scenes) {
         // unknown scene: report like a fault, no steps
-        P.out_d[R.ray] = __builtin_nanf("");
+        store_distance(P, R.ray, __builtin_nanf(""));
         P.out_s[R.ray] = 0;
         if (P.out_steps) P.out_steps[R.ray] = 0;
         return 2;
@@ -584,7 +603,7 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
             const RelaidParams& RP = reload_params();
             int32_t env = 0;
             const uint32_t r = ray_of(RP, tile * 64u + flush_pos, env);
-            __builtin_nontemporal_store(__uint_as_float(tv), &RP.out_d[r]);
+            store_distance(RP, r, __uint_as_float(tv));
             __builtin_nontemporal_store(static_cast<int32_t>(sv), &RP.out_s[r]);
         }
     };
@@ -911,9 +930,8 @@ __device__ __forceinline__ void march_fast(const RelaidParams& P, const SceneLds
                 e[0] = __float_as_uint(t);
                 e[64] = static_cast<uint32_t>(sem);
             } else {
-                // non-temporal: lines of these scattered 4-byte stores do not stay in L2
                 const RelaidParams& RP = reload_params();
-                __builtin_nontemporal_store(t, &RP.out_d[ray]);
+                store_distance(RP, ray, t);
                 __builtin_nontemporal_store(sem, &RP.out_s[ray]);
             }
             if (out_steps) {
@@ -1367,9 +1385,8 @@ __device__ __forceinline__ void march(const RelaidParams& P, SceneLds* lds_scene
             }
         }
         if (finish) {
-            // non-temporal: lines of these scattered 4-byte stores do not stay in L2
             const RelaidParams& RP = reload_params();
-            __builtin_nontemporal_store(t, &RP.out_d[ray]);
+            store_distance(RP, ray, t);
             __builtin_nontemporal_store(sem, &RP.out_s[ray]);
             if (RP.out_steps) RP.out_steps[ray] = step;
         }
@@ -1984,9 +2001,13 @@ extern "C" int navi_trace_relaid_ex(const navi_relaid_launch* L, void* stream) {
     RelaidParams P;
     const int code = relaid_setup(P, L->records, L->n_records, L->scenes, L->n_scenes, L->cell_tables, L->table_depth,
                                   L->env_scene, L->env_order, L->n_envs, L->rays_per_env, L->elevation_bins,
-                                  L->out_distances, L->out_semantics, L->max_steps, L->max_distance,
-                                  L->hit_epsilon, L->out_steps);
-    if (code != NAVI_OK || P.n_rays == 0) return code;
+                                  static_cast<float*>(L->out_distances), L->out_semantics, L->max_steps,
+                                  L->max_distance, L->hit_epsilon, L->out_steps);
+    if (code != NAVI_OK) return code;
+    if (L->distance_dtype != NAVI_DIST_F32 && L->distance_dtype != NAVI_DIST_BF16 && L->distance_dtype != NAVI_DIST_F16)
+        return set_error(NAVI_E_ARG, "distance_dtype must be NAVI_DIST_F32, NAVI_DIST_BF16 or NAVI_DIST_F16");
+    if (P.n_rays == 0) return NAVI_OK;
+    P.dist_dtype = static_cast<uint32_t>(L->distance_dtype);
     if (L->local_dirs) {
         if (!L->env_pos || !L->env_rot) return set_error(NAVI_E_ARG, "env_pos and env_rot must be non-null");
         P.local_dirs = L->local_dirs;

@@ -298,15 +298,19 @@ class ResidentScenes:
 
         ``kernel="relaid"`` (default) runs the device-layout tracer; ``"raw"`` walks the
         reference word layout (and is the one that can fill ``out_words``). Both give
-        identical per-ray results. ``elevation_bins`` declares the canonical
+        identical per-ray results. ``out_distances`` may be float32, bfloat16 or float16
+        (``docs/FUTURE_HARDWARE_ROADMAP.md:140-222`` of the reference: the march keeps float32,
+        a finished ray's distance is rounded to nearest even; record-layout tracer only).
+        ``elevation_bins`` declares the canonical
         ``az * El + el`` ray layout for angular tiling. ``sort_by_scene`` hands the
         envs to the kernel grouped by scene, costliest scenes first once their costs
         are measured (the first such launch counts steps per ray for that)."""
         self._require_gpu()
         e, r = int(origins.shape[0]), int(origins.shape[1])
+        dist_dtype = self._distance_dtype(out_distances)
         for name, t, dt, shape in (("origins", origins, torch.float32, (e, r, 3)),
                                    ("dirs", dirs, torch.float32, (e, r, 3)),
-                                   ("out_distances", out_distances, torch.float32, (e, r)),
+                                   ("out_distances", out_distances, out_distances.dtype, (e, r)),
                                    ("out_semantics", out_semantics, torch.int32, (e, r)),
                                    ("env_scene", env_scene, torch.int32, (e,))):
             if t.device != self.device or t.dtype != dt or not t.is_contiguous() or tuple(t.shape) != shape:
@@ -324,7 +328,8 @@ class ResidentScenes:
             order = self.env_order(env_scene) if sort_by_scene else None
             out_steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
             L = self._launch_args(env_scene.data_ptr(), order, e, r, elevation_bins, out_distances.data_ptr(),
-                                  out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon)
+                                  out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon,
+                                  dist_dtype)
             L.origins, L.dirs = origins.data_ptr(), dirs.data_ptr()
             self._launch(L, e, r, elevation_bins, order)
             if measure:
@@ -332,6 +337,9 @@ class ResidentScenes:
             return
         if kernel not in ("relaid", "raw"):
             raise ValueError(f"unknown kernel {kernel!r}")
+        if dist_dtype != _native.DIST_F32:
+            raise RuntimeError("bfloat16 and float16 distances need the record-layout tracer "
+                               "(kernel='relaid' without out_words, on scenes the record layout holds)")
         if self.pool is None:
             raise RuntimeError("this ResidentScenes keeps no word pool (keep_words=False)")
         with torch.cuda.device(self.device):
@@ -357,6 +365,17 @@ class ResidentScenes:
             raise RuntimeError("these scenes do not fit the device record layout "
                                "(more than 65536 distinct leaves of semantic 0x7fff or above, or 2^27 records)")
 
+    @staticmethod
+    def _distance_dtype(out_distances: Any) -> int:
+        """``navi_relaid_launch.distance_dtype`` of a distance output tensor: float32,
+        bfloat16 or float16 (the march accumulates in float32 either way)."""
+        code = {torch.float32: _native.DIST_F32, torch.bfloat16: _native.DIST_BF16,
+                torch.float16: _native.DIST_F16}.get(getattr(out_distances, "dtype", None))
+        if code is None:
+            raise RuntimeError(f"out_distances must be float32, bfloat16 or float16; got "
+                               f"{getattr(out_distances, 'dtype', None)}")
+        return code
+
     def _check(self, name: str, t: Any, dtype: Any, shape: tuple[int, ...], optional: bool = False) -> int | None:
         if t is None:
             if optional:
@@ -373,23 +392,25 @@ class ResidentScenes:
                         sort_by_scene: bool = True) -> None:
         """Trace with rays generated in the kernel: env ``e`` casts ``local_dirs`` ``[R, 3]``
         rotated by its yaw (``env_rot[e] = (cos, sin)``) from ``env_pos[e]``, the ray layout
-        of ``sdfdag_backend.py:1300-1312``. Outputs ``[E, R]`` as ``cast_rays``."""
+        of ``sdfdag_backend.py:1300-1312``. Outputs ``[E, R]`` as ``cast_rays`` (distances
+        float32, bfloat16 or float16)."""
         self._require_relaid()
         if not 0 < int(max_steps) <= 0x7FFFFFFF:  # an int32 in the C ABI
             raise RuntimeError("max_steps must be a positive integer")
         e, r = int(env_pos.shape[0]), int(local_dirs.shape[0])
+        dist_dtype = self._distance_dtype(out_distances)
         ptrs = [self._check("env_scene", env_scene, torch.int32, (e,)),
                 self._check("local_dirs", local_dirs, torch.float32, (r, 3)),
                 self._check("env_pos", env_pos, torch.float32, (e, 3)),
                 self._check("env_rot", env_rot, torch.float32, (e, 2)),
-                self._check("out_distances", out_distances, torch.float32, (e, r)),
+                self._check("out_distances", out_distances, out_distances.dtype, (e, r)),
                 self._check("out_semantics", out_semantics, torch.int32, (e, r)),
                 self._check("out_steps", out_steps, torch.int32, (e, r), optional=True)]
         self._poll_cost()
         order = self.env_order(env_scene) if sort_by_scene else None
         steps, measure = self._cost_steps(out_steps, e, r, sort_by_scene)
         L = self._launch_args(ptrs[0], order, e, r, elevation_bins, ptrs[4], ptrs[5], steps, max_steps,
-                              max_distance, hit_epsilon)
+                              max_distance, hit_epsilon, dist_dtype)
         L.local_dirs, L.env_pos, L.env_rot = ptrs[1], ptrs[2], ptrs[3]
         self._launch(L, e, r, elevation_bins, order)
         if measure:
@@ -398,7 +419,7 @@ class ResidentScenes:
     # ---- launches ----
 
     def _launch_args(self, env_scene_ptr, order, e, r, elevation_bins, out_d_ptr, out_s_ptr, steps, max_steps,
-                     max_distance, hit_epsilon) -> Any:
+                     max_distance, hit_epsilon, dist_dtype: int = 0) -> Any:
         L = _native.RelaidLaunch()
         L.records, L.n_records = self.records.data_ptr(), self.n_records
         if self.n_leaves:
@@ -411,6 +432,7 @@ class ResidentScenes:
         L.out_distances, L.out_semantics = out_d_ptr, out_s_ptr
         L.out_steps = steps.data_ptr() if steps is not None else None
         L.max_steps, L.max_distance, L.hit_epsilon = int(max_steps), float(max_distance), float(hit_epsilon)
+        L.distance_dtype = int(dist_dtype)
         return L
 
     def _launch(self, L, e: int, r: int, elevation_bins, order) -> None:

@@ -26,6 +26,7 @@ except ImportError:
 
 _DAG_DTYPE = torch.int64
 _DISTANCE_DTYPE = torch.float32
+_DISTANCE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)  # out_distances
 _SEMANTIC_DTYPE = torch.int32
 _HIT_EPSILON = 0.01  # kernel.cuh:7
 _DIRECTION_NORM_EPS = 1e-4  # kernel.cuh:9
@@ -81,7 +82,12 @@ def _validate_cast_rays_inputs(dag_tensor: Any, origins: Any, dirs: Any, out_dis
         )
     _validate_cuda_tensor(origins, name="origins", dtype=_DISTANCE_DTYPE)
     _validate_cuda_tensor(dirs, name="dirs", dtype=_DISTANCE_DTYPE)
-    _validate_cuda_tensor(out_distances, name="out_distances", dtype=_DISTANCE_DTYPE,
+    # float32, or the reference roadmap's bfloat16 / float16 distances
+    # (docs/FUTURE_HARDWARE_ROADMAP.md:157-176): validated against the tensor's own dtype
+    # when it is one of those, so any other dtype gets the float32 message
+    _validate_cuda_tensor(out_distances, name="out_distances",
+                          dtype=out_distances.dtype if getattr(out_distances, "dtype", None) in _DISTANCE_DTYPES
+                          else _DISTANCE_DTYPE,
                           shape=(batch, rays))
     _validate_cuda_tensor(out_semantics, name="out_semantics", dtype=_SEMANTIC_DTYPE,
                           shape=(batch, rays))

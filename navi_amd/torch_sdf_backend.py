@@ -13,7 +13,10 @@ Additions, all keyword-only so the positional contract is unchanged:
 ``hit_epsilon`` (the reference's compile-time ``kHitEpsilon``, ``kernel.cuh:7``),
 ``out_steps`` (an int32 ``[B, R]`` tensor receiving per-ray step counts),
 ``elevation_bins`` (declares the canonical ``az * El + el`` ray order so rays are
-traced in angular tiles) and ``kernel``.
+traced in angular tiles) and ``kernel``. ``out_distances`` may also be bfloat16 or
+float16, the reference roadmap's T2 item (``docs/FUTURE_HARDWARE_ROADMAP.md:140-222``):
+the march accumulates in float32 and each finished ray's distance is rounded to nearest
+even (record-layout tracer only; a call that would take the word-layout kernel raises).
 
 Kernels. ``kernel="auto"`` (default) traces with the record-layout tracer
 (``navi_trace_relaid``) over a record-layout copy of the DAG tensor: its words
@@ -56,6 +59,7 @@ _DIRECTION_NORM_EPS = 1e-4  # kernel.cuh:9
 HIT_EPSILON = 0.01  # kernel.cuh:7
 _INT32_MAX = 0x7FFFFFFF
 RELAID_MAX_RAYS = 1 << 30  # rays per navi_trace_relaid launch; larger batches take navi_cast_rays
+_DISTANCE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
 __all__ = ["cast_rays", "prepare", "invalidate", "conversion_counts", "LayoutConversionWarning", "HIT_EPSILON"]
 
@@ -118,7 +122,9 @@ def validate_cast_inputs(dag_tensor, origins, dirs, out_distances, out_semantics
     _check(dag_tensor.dtype == torch.int64, "dag_tensor must be int64")
     _check(origins.dtype == torch.float32, "origins must be float32")
     _check(dirs.dtype == torch.float32, "dirs must be float32")
-    _check(out_distances.dtype == torch.float32, "out_distances must be float32")
+    # float32 as bindings.cpp:71; bfloat16 and float16 are the reference roadmap's
+    # extension of this check (docs/FUTURE_HARDWARE_ROADMAP.md:157-176)
+    _check(out_distances.dtype in _DISTANCE_DTYPES, "out_distances must be float32 or bfloat16 (or float16)")
     _check(out_semantics.dtype == torch.int32, "out_semantics must be int32")
 
     _check(origins.dim() == 3 and origins.size(2) == 3, "origins must be [Batch, Rays, 3]")
@@ -257,10 +263,16 @@ def cast_rays(
     dev = dag_tensor.device
     scenes = (_record_layout(dag_tensor, bbox_min, bbox_max, "cast_rays")
               if kernel == "auto" and n_rays <= RELAID_MAX_RAYS else None)
+    dist_dtype = scenes._distance_dtype(out_distances) if scenes is not None else _native.DIST_F32
+    if out_distances.dtype != torch.float32 and scenes is None:
+        raise RuntimeError("bfloat16 and float16 distances need the record-layout tracer (kernel='auto', a DAG "
+                           "the record layout holds, at most 2^30 rays); this call would take the word-layout "
+                           "kernel, which writes float32")
     if scenes is not None:
         # one scene, no scene table or env order (navi_trace_relaid_ex, leaf table included)
         L = scenes._launch_args(None, None, n_envs, rays, elevation_bins, out_distances.data_ptr(),
-                                out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon)
+                                out_semantics.data_ptr(), out_steps, max_steps, max_distance, hit_epsilon,
+                                dist_dtype)
         L.origins, L.dirs = origins.data_ptr(), dirs.data_ptr()
         with torch.cuda.device(dev):
             stream = torch.cuda.current_stream(dev).cuda_stream

@@ -93,6 +93,37 @@ def test_python_layer_rejections(fake_gpu, over, args, msg):
         backend_module.cast_rays(*_inputs(**over), *args, skip_direction_validation=True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_reduced_precision_distances_pass_the_python_layer(monkeypatch, dtype):
+    """out_distances may be bfloat16 or float16 (the reference roadmap's T2 item,
+    docs/FUTURE_HARDWARE_ROADMAP.md:157-176); the native call gets the tensor as is."""
+    captured = {}
+
+    class _Backend:
+        def cast_rays(self, *args, **kw):
+            captured["dtype"] = args[3].dtype
+
+    monkeypatch.setattr(backend_module, "HAS_CUDA_BACKEND", True)
+    monkeypatch.setattr(backend_module, "torch_sdf_backend", _Backend())
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: True)
+    backend_module.cast_rays(*_inputs(out_distances=_FakeTensor(shape=(2, 3), dtype=dtype)), 64, 17.5,
+                             [0, 0, 0], [1, 1, 1], 128, skip_direction_validation=True)
+    assert captured["dtype"] == dtype
+
+
+def test_other_distance_dtypes_are_rejected(fake_gpu):
+    for dtype in (torch.float64, torch.int32):
+        with pytest.raises(RuntimeError, match="out_distances must have dtype torch.float32"):
+            backend_module.cast_rays(*_inputs(out_distances=_FakeTensor(shape=(2, 3), dtype=dtype)), 64, 30.0,
+                                     [0, 0, 0], [1, 1, 1], 128, skip_direction_validation=True)
+    # the native layer's message keeps the reference's prefix (bindings.cpp:71)
+    with pytest.raises(RuntimeError, match="out_distances must be float32"):
+        torch_sdf_backend.validate_cast_inputs(
+            *[_FakeTensor(shape=t.shape, dtype=t.dtype, is_cuda=True) for t in _inputs()[:3]],
+            _FakeTensor(shape=(2, 3), dtype=torch.float64), _FakeTensor(shape=(2, 3), dtype=torch.int32),
+            64, 30.0, [0, 0, 0], [1, 1, 1], 128)
+
+
 def test_direction_norm_checks():
     with pytest.raises(RuntimeError, match="normalized within tolerance"):
         backend_module._validate_direction_norms(torch.tensor([[[1.2, 0.0, 0.0]]]))
