@@ -702,6 +702,22 @@ def main() -> int:
             (timed_d.view(np.uint32) != out_d.cpu().numpy().view(np.uint32)) | (timed_s != out_s.cpu().numpy())))
         _log(f"headline parity {par}")
 
+    # the same launches writing bfloat16 distances (the reference roadmap's T2 output):
+    # timed alike, and every distance against the float32 launch's rounded to bfloat16
+    out_bf = torch.empty((E, R), device=dev, dtype=torch.bfloat16)
+    res.cast_rays(t_es, t_o, t_d, out_bf, out_s, args.max_steps, args.max_distance, elevation_bins=W.EL)
+    bf_launches = time_launches(
+        lambda: res.cast_rays(t_es, t_o, t_d, out_bf, out_s, args.max_steps, args.max_distance,
+                              elevation_bins=W.EL), 20, 3)
+    want_bf = torch.from_numpy(timed_d).to(dev).to(torch.bfloat16)
+    nan_bf = torch.isnan(want_bf)
+    bf16 = {"ms": round(float(np.median(bf_launches)), 4),
+            "rays_per_s": round(n_rays / (float(np.median(bf_launches)) / 1e3), 1),
+            "mismatch_vs_float32_rounded": int(((out_bf.view(torch.int16) != want_bf.view(torch.int16)) & ~nan_bf)
+                                               .sum().item() + (torch.isnan(out_bf) != nan_bf).sum().item()),
+            "output_bytes": n_rays * 2}
+    del out_bf, want_bf, nan_bf
+
     small = obs = dropin = None
     if not args.headline_only:
         small = []
@@ -746,6 +762,7 @@ def main() -> int:
         "small_configs": small,
         "observation_step": obs,
         "dropin_cast_rays": dropin,
+        "bf16_distances": bf16,
         "scene_compile_s": round(t_compile, 2),
     }
     print(json.dumps(line), flush=True)
