@@ -250,3 +250,54 @@ def test_headers_compile_on_their_own(tmp_path, header, lang):
     out = subprocess.run([compiler, std, "-Wall", "-Wextra", "-pedantic", "-Werror", "-fsyntax-only",
                           "-I", str(ROOT / "include"), str(src)], capture_output=True, text=True)
     assert out.returncode == 0, out.stderr
+
+
+def test_ctypes_structs_match_the_header(tmp_path):
+    """Every struct the Python layer passes through the C ABI has the header's size and
+    field offsets (gcc on include/navi_trace.h against ctypes), so a field added on one
+    side only fails here rather than on the device."""
+    import shutil
+    import subprocess
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not installed")
+    structs = {"navi_relaid_launch": _native.RelaidLaunch, "navi_point_queries": _native.PointQueries,
+               "navi_observation": _native.Observation, "navi_launch_info": _native.LaunchInfo}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "navi_trace.h"', "int main(void) {"]
+    for cname, cls in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines += ['  printf("navi_relaid_scene size %zu\\n", sizeof(navi_relaid_scene));',
+              '  printf("navi_scene_desc size %zu\\n", sizeof(navi_scene_desc));', "  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    got = {tuple(line.split()[:2]): int(line.split()[2]) for line in out if line}
+    for cname, cls in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(cls), cname
+        for field, _ in cls._fields_:
+            assert got[(cname, field)] == getattr(cls, field).offset, (cname, field)
+    assert got[("navi_relaid_scene", "size")] == 48 and got[("navi_scene_desc", "size")] == 40
+
+
+def test_relaid_ex_rejects_bad_arguments_without_a_gpu():
+    lib = _native.lib()
+    assert lib.navi_trace_relaid_ex(None, None) == _native.NAVI_E_ARG
+    assert "launch" in _native.last_error()
+    base = dict(records=1, n_records=1, scenes=1, n_scenes=1, cell_tables=1, table_depth=6, n_envs=0,
+                rays_per_env=4, max_steps=4, max_distance=1.0, hit_epsilon=0.01)
+    # an empty batch is accepted, but not with an unknown distance type
+    assert lib.navi_trace_relaid_ex(ctypes.byref(_native.RelaidLaunch(**base)), None) == _native.NAVI_OK
+    for bad in (3, -1):
+        L = _native.RelaidLaunch(**base, distance_dtype=bad)
+        assert lib.navi_trace_relaid_ex(ctypes.byref(L), None) == _native.NAVI_E_ARG
+        assert "distance_dtype" in _native.last_error()
+    L = _native.RelaidLaunch(**dict(base, n_envs=1, out_distances=1, out_semantics=1))
+    assert lib.navi_trace_relaid_ex(ctypes.byref(L), None) == _native.NAVI_E_ARG
+    assert "origins and dirs" in _native.last_error()
+    L = _native.RelaidLaunch(**dict(base, n_envs=1, out_distances=1, out_semantics=1, local_dirs=1))
+    assert lib.navi_trace_relaid_ex(ctypes.byref(L), None) == _native.NAVI_E_ARG
+    assert "env_pos" in _native.last_error()
